@@ -1,0 +1,173 @@
+/*
+ * nvk.h — C ABI of the MI355X (gfx950) KV-cache hot path of nano-vLLM.
+ *
+ * Three entry points replace the three GPU calls that
+ * nanovllm/layers/attention.py makes per decoder layer:
+ *
+ *   nvk_kv_store        <- store_kvcache_kernel / store_kvcache
+ *                          (nanovllm/layers/attention.py:10-40)
+ *   nvk_paged_decode    <- flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
+ *                          cache_seqlens=context_lens, block_table=block_tables,
+ *                          softmax_scale, causal=True)
+ *                          (nanovllm/layers/attention.py:72-74)
+ *   nvk_varlen_prefill  <- flash_attn_varlen_func(q, k, v, max_seqlen_q, cu_seqlens_q,
+ *                          max_seqlen_k, cu_seqlens_k, softmax_scale, causal=True,
+ *                          block_table)
+ *                          (nanovllm/layers/attention.py:64-70)
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers (hipMalloc / torch CUDA tensors) except
+ *     where stated.  Strides are in ELEMENTS, not bytes.
+ *   - Nothing is allocated and nothing is synchronised: the work is enqueued on
+ *     `stream` (a hipStream_t passed as void*; NULL = the null stream), so every
+ *     entry point may be captured into a hipGraph.  No device metadata is read
+ *     on the host.
+ *   - Return value: 0 = enqueued; a negative NVK_E* code = the arguments were
+ *     rejected before anything was launched; a positive value = the hipError_t
+ *     reported by the launch.
+ *   - The library keeps no pointer after it returns and has no global state,
+ *     so calls from several host threads on distinct streams are independent.
+ *   - KV-cache layout (nanovllm/engine/model_runner.py:115-121): per layer
+ *     k_cache / v_cache are contiguous [num_blocks][block_size][num_kv_heads][head_dim];
+ *     the flat token slot s = page * block_size + offset addresses row s of a
+ *     [num_blocks*block_size][num_kv_heads*head_dim] view.
+ */
+#ifndef NVK_H_
+#define NVK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* error codes (negative; positive values are hipError_t) */
+#define NVK_OK 0
+#define NVK_EINVAL (-1)       /* null pointer, negative size, inconsistent shape   */
+#define NVK_EUNSUPPORTED (-2) /* head_dim / group size / dtype not built          */
+#define NVK_EALIGN (-3)       /* pointer or stride misaligned for the element type */
+#define NVK_EWORKSPACE (-4)   /* workspace missing or smaller than required       */
+
+/* element types of q / k / v / caches / outputs */
+#define NVK_DTYPE_BF16 0
+#define NVK_DTYPE_F16 1
+#define NVK_DTYPE_F32 2
+
+/* Human-readable text for an NVK_E* code or a hipError_t. Never NULL. */
+const char* nvk_strerror(int code);
+
+/* gfx target the library was built for, e.g. "gfx950". */
+const char* nvk_build_target(void);
+
+/*
+ * KV-store scatter.
+ * Replaces store_kvcache_kernel (nanovllm/layers/attention.py:10-30) and its
+ * launcher store_kvcache (attention.py:33-40).
+ *
+ * For every token t in [0, n_tokens):
+ *     s = slot_mapping[t];
+ *     if s == -1: skip                                  (attention.py:22-23)
+ *     k_cache[s*row_elems : (s+1)*row_elems] = key  [t*key_row_stride   : +row_elems]
+ *     v_cache[s*row_elems : (s+1)*row_elems] = value[t*value_row_stride : +row_elems]
+ *
+ * row_elems = num_kv_heads*head_dim (the Triton kernel's D).  Each token row of
+ * key / value must be contiguous (the reference asserts stride(-1)==1 and
+ * stride(1)==head_dim, attention.py:36-37); the row strides are free, which
+ * covers the value view of the packed qkv (row stride (Hq+2*Hkv)*head_dim).
+ * cache_slots = num_blocks*block_size.  A slot outside [0, cache_slots) is
+ * skipped like -1: the reference writes out of bounds there, this library
+ * writes nothing.  Duplicate slots are a race (one of the rows wins), never a
+ * fault.  elem_bytes is 2 (bf16/f16) or 4 (f32).
+ */
+int nvk_kv_store(const void* key, int64_t key_row_stride,
+                 const void* value, int64_t value_row_stride,
+                 void* k_cache, void* v_cache,
+                 const int32_t* slot_mapping, int64_t n_tokens,
+                 int32_t row_elems, int32_t elem_bytes, int64_t cache_slots,
+                 void* stream);
+
+/*
+ * Paged GQA decode attention, one query token per sequence.
+ * Replaces flash_attn_with_kvcache(q.unsqueeze(1), k_cache, v_cache,
+ *     cache_seqlens=context_lens, block_table=block_tables,
+ *     softmax_scale=scale, causal=True)      (nanovllm/layers/attention.py:72-74)
+ *
+ *   out[b, h, :] = softmax_j( scale * q[b,h,:] . K[b, j, h/G, :] ) V[b, j, h/G, :]
+ *   over j < context_lens[b], with K[b, j] = k_cache[block_tables[b, j/block_size]]
+ *   [j % block_size] and G = num_q_heads / num_kv_heads.
+ *
+ * q:   [batch][num_q_heads][head_dim] with strides (q_stride_tok, q_stride_head, 1).
+ * out: same shape, strides (out_stride_tok, out_stride_head, 1).
+ * block_tables: int32 [batch][max_blocks] with row stride bt_stride; entries at
+ *   or beyond ceil(context_lens[b]/block_size) are never read (they may be -1
+ *   or stale, model_runner.py:123-127, 204-211).
+ * context_lens: int32 [batch]; it counts the token just stored
+ *   (model_runner.py:180).  context_lens[b] == 0 (a padded graph row) writes
+ *   zeros.  Lengths above max_blocks*block_size are clamped to it; page ids
+ *   outside [0, num_blocks) contribute no keys.
+ * workspace: device scratch of nvk_paged_decode_workspace_size() bytes
+ *   (split-K partial results); it need not be initialised.
+ * scale must be > 0.  dtype: NVK_DTYPE_BF16.  head_dim: 128 or 64.
+ * G: 1, 2, 4 or 8.
+ */
+int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                     const void* k_cache, const void* v_cache,
+                     const int32_t* block_tables, int64_t bt_stride,
+                     const int32_t* context_lens,
+                     int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t block_size, int32_t max_blocks,
+                     int32_t num_blocks, float scale,
+                     void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                     void* workspace, size_t workspace_bytes,
+                     int32_t dtype, void* stream);
+
+/* Bytes of workspace nvk_paged_decode needs for these sizes (0 on bad input). */
+size_t nvk_paged_decode_workspace_size(int32_t batch, int32_t num_q_heads,
+                                       int32_t head_dim, int32_t block_size,
+                                       int32_t max_blocks);
+
+/*
+ * Varlen causal attention over new tokens, with or without a paged prefix.
+ * Replaces flash_attn_varlen_func(q, k, v, max_seqlen_q=..., cu_seqlens_q=...,
+ *     max_seqlen_k=..., cu_seqlens_k=..., softmax_scale=scale, causal=True,
+ *     block_table=block_tables)               (nanovllm/layers/attention.py:64-70)
+ *
+ * Sequence s has Lq = cu_seqlens_q[s+1]-cu_seqlens_q[s] query rows and
+ * Lk = cu_seqlens_k[s+1]-cu_seqlens_k[s] keys.  Query row i sees key j iff
+ * j <= i + Lk - Lq (bottom-right aligned causal mask, the flash-attn 2.x
+ * convention); a row that sees no key is written as zeros.
+ *
+ * q:   [total_q][num_q_heads][head_dim], strides (q_stride_tok, q_stride_head, 1).
+ * out: [total_q][num_q_heads][head_dim], strides (out_stride_tok, out_stride_head, 1).
+ * Paged mode (block_tables != NULL): k / v are the caches
+ *   [num_blocks][block_size][num_kv_heads][head_dim] (contiguous; k_stride_tok,
+ *   v_stride_tok and kv_stride_head are ignored) and key j of sequence s lives
+ *   in page block_tables[s*bt_stride + j/block_size].  Lk is clamped to
+ *   max_blocks*block_size; page ids outside [0, num_blocks) contribute no keys.
+ * Dense mode (block_tables == NULL): k / v are [total_k][num_kv_heads][head_dim]
+ *   with row strides k_stride_tok / v_stride_tok and head stride kv_stride_head;
+ *   key j of sequence s is row cu_seqlens_k[s] + j (rows >= total_k are
+ *   treated as absent).
+ * max_seqlen_q sizes the grid (host value, as in the reference's Context).
+ * scale must be > 0.  dtype: NVK_DTYPE_BF16.  head_dim: 128.  G: 1, 2, 4 or 8.
+ */
+int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                       int64_t total_q,
+                       const void* k, const void* v,
+                       int64_t k_stride_tok, int64_t v_stride_tok,
+                       int64_t kv_stride_head, int64_t total_k,
+                       const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                       int32_t batch, int32_t max_seqlen_q,
+                       const int32_t* block_tables, int64_t bt_stride,
+                       int32_t max_blocks, int32_t block_size, int32_t num_blocks,
+                       int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                       float scale,
+                       void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                       int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NVK_H_ */

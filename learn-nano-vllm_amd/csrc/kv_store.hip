@@ -1,0 +1,137 @@
+// KV-store scatter: the slot_mapping copy of new key/value rows into the
+// paged cache.  Same semantics as store_kvcache_kernel
+// (nanovllm/layers/attention.py:10-30): slot -1 skips the token, otherwise
+// the token's K row and V row are copied to row `slot` of the flat cache.
+//
+// Mapping (MI355X): the work is a pure HBM copy of 2 * row_bytes per valid
+// token.  One thread owns one VEC-byte chunk at the same offset of the K row
+// and of the V row, so each thread has two independent loads in flight before
+// its two stores, and a 256-thread workgroup covers 256/chunks_per_row whole
+// tokens (2 tokens for a 2 KiB Qwen3-0.6B row).  A token whose slot is -1
+// costs one 4-byte slot read per thread group.  With 16-byte chunks the
+// 4096-token layer step is 2048 workgroups, i.e. every CU of the part holds
+// its share of the copy from the first wave of dispatch.
+#include "nvk_common.h"
+
+namespace {
+
+template <typename VecT>
+__global__ __launch_bounds__(256) void kv_store_rows_kernel(
+    const char* __restrict__ key, int64_t key_stride_bytes,
+    const char* __restrict__ value, int64_t value_stride_bytes,
+    char* __restrict__ k_cache, char* __restrict__ v_cache,
+    const int32_t* __restrict__ slot_mapping, int64_t n_tokens,
+    int64_t row_bytes, int chunk_shift, int64_t cache_slots) {
+  // chunk_shift = log2(chunks_per_row); 256 >> chunk_shift tokens per workgroup.
+  const int tid = threadIdx.x;
+  const int64_t token = (int64_t)blockIdx.x * (256 >> chunk_shift) + (tid >> chunk_shift);
+  const int chunk = tid & ((1 << chunk_shift) - 1);
+  if (token >= n_tokens) return;
+  const int32_t slot = slot_mapping[token];
+  if (slot < 0 || (int64_t)slot >= cache_slots) return;
+  const VecT kx = reinterpret_cast<const VecT*>(key + token * key_stride_bytes)[chunk];
+  const VecT vx = reinterpret_cast<const VecT*>(value + token * value_stride_bytes)[chunk];
+  const int64_t dst = (int64_t)slot * row_bytes;
+  reinterpret_cast<VecT*>(k_cache + dst)[chunk] = kx;
+  reinterpret_cast<VecT*>(v_cache + dst)[chunk] = vx;
+}
+
+// Any row size: one workgroup per token, threads stride over the row's chunks.
+template <typename VecT>
+__global__ __launch_bounds__(256) void kv_store_generic_kernel(
+    const char* __restrict__ key, int64_t key_stride_bytes,
+    const char* __restrict__ value, int64_t value_stride_bytes,
+    char* __restrict__ k_cache, char* __restrict__ v_cache,
+    const int32_t* __restrict__ slot_mapping, int64_t n_tokens,
+    int64_t row_bytes, int64_t cache_slots) {
+  const int64_t token = blockIdx.x;
+  if (token >= n_tokens) return;
+  const int32_t slot = slot_mapping[token];
+  if (slot < 0 || (int64_t)slot >= cache_slots) return;
+  const int64_t nchunks = row_bytes / (int64_t)sizeof(VecT);
+  const VecT* ks = reinterpret_cast<const VecT*>(key + token * key_stride_bytes);
+  const VecT* vs = reinterpret_cast<const VecT*>(value + token * value_stride_bytes);
+  VecT* kd = reinterpret_cast<VecT*>(k_cache + (int64_t)slot * row_bytes);
+  VecT* vd = reinterpret_cast<VecT*>(v_cache + (int64_t)slot * row_bytes);
+  for (int64_t c = threadIdx.x; c < nchunks; c += blockDim.x) {
+    const VecT kx = ks[c];
+    const VecT vx = vs[c];
+    kd[c] = kx;
+    vd[c] = vx;
+  }
+}
+
+inline bool aligned_to(const void* p, int64_t a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
+
+template <typename VecT>
+int launch_kv_store(const char* key, int64_t ksb, const char* value, int64_t vsb, char* kc,
+                    char* vc, const int32_t* slots, int64_t n_tokens, int64_t row_bytes,
+                    int64_t cache_slots, hipStream_t stream) {
+  const int64_t cpr = row_bytes / (int64_t)sizeof(VecT);
+  const int shift = nvk_log2_exact((int)(cpr <= 256 ? cpr : 0));
+  if (shift >= 0) {
+    const int64_t tpb = 256 >> shift;
+    const int64_t grid = (n_tokens + tpb - 1) / tpb;
+    hipLaunchKernelGGL(kv_store_rows_kernel<VecT>, dim3((unsigned)grid), dim3(256), 0, stream,
+                       key, ksb, value, vsb, kc, vc, slots, n_tokens, row_bytes, shift,
+                       cache_slots);
+  } else {
+    hipLaunchKernelGGL(kv_store_generic_kernel<VecT>, dim3((unsigned)n_tokens), dim3(256), 0,
+                       stream, key, ksb, value, vsb, kc, vc, slots, n_tokens, row_bytes,
+                       cache_slots);
+  }
+  return nvk_launch_status();
+}
+
+}  // namespace
+
+extern "C" int nvk_kv_store(const void* key, int64_t key_row_stride, const void* value,
+                            int64_t value_row_stride, void* k_cache, void* v_cache,
+                            const int32_t* slot_mapping, int64_t n_tokens, int32_t row_elems,
+                            int32_t elem_bytes, int64_t cache_slots, void* stream) {
+  if (n_tokens < 0 || row_elems <= 0 || cache_slots < 0) return NVK_EINVAL;
+  if (elem_bytes != 2 && elem_bytes != 4) return NVK_EUNSUPPORTED;
+  if (n_tokens == 0) return NVK_OK;
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping) return NVK_EINVAL;
+  if (key_row_stride < row_elems || value_row_stride < row_elems) return NVK_EINVAL;
+  if (n_tokens > (int64_t)INT32_MAX) return NVK_EINVAL;
+  if (!aligned_to(slot_mapping, 4)) return NVK_EALIGN;
+
+  const int64_t row_bytes = (int64_t)row_elems * elem_bytes;
+  const int64_t ksb = key_row_stride * elem_bytes;
+  const int64_t vsb = value_row_stride * elem_bytes;
+  auto fits = [&](int64_t a) {
+    return row_bytes % a == 0 && ksb % a == 0 && vsb % a == 0 && aligned_to(key, a) &&
+           aligned_to(value, a) && aligned_to(k_cache, a) && aligned_to(v_cache, a);
+  };
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const char* kp = static_cast<const char*>(key);
+  const char* vp = static_cast<const char*>(value);
+  char* kcp = static_cast<char*>(k_cache);
+  char* vcp = static_cast<char*>(v_cache);
+  if (fits(16))
+    return launch_kv_store<uint4>(kp, ksb, vp, vsb, kcp, vcp, slot_mapping, n_tokens, row_bytes,
+                                  cache_slots, s);
+  if (fits(4))
+    return launch_kv_store<uint32_t>(kp, ksb, vp, vsb, kcp, vcp, slot_mapping, n_tokens,
+                                     row_bytes, cache_slots, s);
+  if (fits(2))
+    return launch_kv_store<uint16_t>(kp, ksb, vp, vsb, kcp, vcp, slot_mapping, n_tokens,
+                                     row_bytes, cache_slots, s);
+  return NVK_EALIGN;
+}
+
+extern "C" const char* nvk_strerror(int code) {
+  switch (code) {
+    case NVK_OK: return "ok";
+    case NVK_EINVAL: return "nvk: invalid argument (null pointer, negative size or inconsistent shape)";
+    case NVK_EUNSUPPORTED: return "nvk: unsupported head_dim / group size / dtype";
+    case NVK_EALIGN: return "nvk: pointer or stride misaligned for the element type";
+    case NVK_EWORKSPACE: return "nvk: workspace missing or too small";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+  return "nvk: unknown error";
+}
+
+extern "C" const char* nvk_build_target(void) { return "gfx950"; }

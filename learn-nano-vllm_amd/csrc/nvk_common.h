@@ -1,0 +1,101 @@
+// Device helpers shared by the nvk kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nvk.h"
+
+#define NVK_DEVICE __device__ __forceinline__
+
+typedef __bf16 nvk_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 nvk_bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 nvk_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float nvk_f32x4 __attribute__((ext_vector_type(4)));
+typedef float nvk_f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t nvk_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t nvk_u32x2 __attribute__((ext_vector_type(2)));
+
+// log2(e): softmax is evaluated as exp2(x*log2e - m), v_exp_f32 being base 2.
+#define NVK_LOG2E 1.4426950408889634f
+
+// ---- launch-status helper -------------------------------------------------
+static inline int nvk_launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? NVK_OK : (int)e;
+}
+
+// ---- bf16 <-> f32 ----------------------------------------------------------
+// bf16 is the high half of an f32: widening is a shift / mask.
+NVK_DEVICE float nvk_bf16lo_to_f32(uint32_t w) { return __uint_as_float(w << 16); }
+NVK_DEVICE float nvk_bf16hi_to_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even pack of two f32 into one bf16x2 word (v_cvt_pk_bf16_f32).
+NVK_DEVICE uint32_t nvk_pack_bf16x2(float lo, float hi) {
+  nvk_bf16x2 p = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+// a.lo*b.lo + a.hi*b.hi + c with f32 accumulation (v_dot2_f32_bf16).
+NVK_DEVICE float nvk_dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(nvk_bf16x2, a),
+                                         __builtin_bit_cast(nvk_bf16x2, b), c, false);
+}
+
+// ---- cross-lane reductions -------------------------------------------------
+// DPP controls (GFX9 encoding): quad_perm xor1 / xor2, row_half_mirror, row_mirror.
+#define NVK_DPP_QP_XOR1 0xB1
+#define NVK_DPP_QP_XOR2 0x4E
+#define NVK_DPP_HALF_MIRROR 0x141
+#define NVK_DPP_MIRROR 0x140
+
+template <int CTRL>
+NVK_DEVICE float nvk_dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over aligned groups of LANES consecutive lanes (LANES in {4, 8, 16});
+// every lane of the group receives the group total.
+template <int LANES>
+NVK_DEVICE float nvk_group_sum(float x) {
+  static_assert(LANES == 4 || LANES == 8 || LANES == 16, "group size");
+  x += nvk_dpp<NVK_DPP_QP_XOR1>(x);
+  x += nvk_dpp<NVK_DPP_QP_XOR2>(x);
+  if constexpr (LANES >= 8) x += nvk_dpp<NVK_DPP_HALF_MIRROR>(x);
+  if constexpr (LANES >= 16) x += nvk_dpp<NVK_DPP_MIRROR>(x);
+  return x;
+}
+
+// Value of lane (lane ^ MASK) for MASK in {16, 32} (ds_swizzle-free: bpermute).
+template <int MASK>
+NVK_DEVICE float nvk_xor_lane(float x) {
+  const int lane = __lane_id();
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ MASK) << 2, __float_as_int(x)));
+}
+
+NVK_DEVICE float nvk_fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---- integer helpers ---------------------------------------------------------
+// Page lookup for key position `pos` of a sequence: returns the flat cache row
+// (page*block_size + offset) or -1 when the page id is outside [0, num_blocks).
+NVK_DEVICE int64_t nvk_paged_row(const int32_t* __restrict__ bt_row, int pos, int block_size,
+                                 int bs_shift, int num_blocks) {
+  int logical, offset;
+  if (bs_shift >= 0) {
+    logical = pos >> bs_shift;
+    offset = pos & (block_size - 1);
+  } else {
+    logical = pos / block_size;
+    offset = pos - logical * block_size;
+  }
+  const int page = bt_row[logical];
+  if (page < 0 || page >= num_blocks) return -1;
+  return (int64_t)page * block_size + offset;
+}
+
+static inline int nvk_log2_exact(int v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int s = 0;
+  while ((1 << s) < v) ++s;
+  return s;
+}

@@ -1,0 +1,218 @@
+"""Seeded synthetic inputs of the KV-cache path at Qwen3-0.6B shape.
+
+Five workloads (16 q heads, 8 kv heads, head_dim 128, bf16, 256-token pages):
+
+  kv_store_case     4096 new tokens scattered into a 64-page cache; the slots are
+                    the first 4096 of a random permutation of the 16384 slots, with
+                    205 (5 %) of them set to -1.
+  decode_case       64 sequences, context U{100..2048}, pages drawn without
+                    sharing from a shuffled 1024-page pool, tables padded with -1.
+  prefill_case      32 sequences = a shared 512-token prefix (2 common pages) plus
+                    U{100..1024} new tokens in fresh pages; the new K/V are stored
+                    through slot_mapping before attention.
+  spec_verify_case  32 sequences, context U{1024..8192} of which the last 6 are
+                    queries; the last 5 (draft tokens) are stored in the step.
+  mixed_layer_case  one layer of a chunked-prefill + decode step: 8 chunks of 512
+                    new tokens after U{0..1536} cached ones, plus 192 decodes with
+                    context U{256..4096}.
+
+Every tensor is produced on the CPU from ``torch.Generator().manual_seed(seed)``
+in a fixed order, so a case is identical wherever it is built; ``.to(device)``
+moves it.  Values are N(0,1) rounded to bf16.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+HQ, HKV, HD, BLOCK = 16, 8, 128, 256
+
+
+def _randn(gen, *shape):
+    return torch.randn(*shape, generator=gen, dtype=torch.float32).to(torch.bfloat16)
+
+
+def _randint(gen, lo, hi, n):
+    """n integers uniform in [lo, hi] (inclusive)."""
+    return torch.randint(lo, hi + 1, (n,), generator=gen).tolist()
+
+
+def _pad_tables(tables, width=None):
+    w = width if width is not None else max(len(t) for t in tables)
+    out = torch.full((len(tables), w), -1, dtype=torch.int32)
+    for i, t in enumerate(tables):
+        out[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    return out
+
+
+@dataclass
+class Case:
+    tensors: dict = field(default_factory=dict)
+    meta: dict = field(default_factory=dict)
+
+    def __getattr__(self, name):
+        t = self.__dict__.get("tensors", {})
+        if name in t:
+            return t[name]
+        m = self.__dict__.get("meta", {})
+        if name in m:
+            return m[name]
+        raise AttributeError(name)
+
+    def to(self, device):
+        return Case({k: (v.to(device) if isinstance(v, torch.Tensor) else v)
+                     for k, v in self.tensors.items()}, dict(self.meta))
+
+
+def kv_store_case(seed=0, n_tokens=4096, num_blocks=64, block_size=BLOCK, hkv=HKV, hd=HD,
+                  skip=205, value_row_stride=None):
+    gen = torch.Generator().manual_seed(seed)
+    key = _randn(gen, n_tokens, hkv, hd)
+    value_full = _randn(gen, n_tokens, (value_row_stride or hkv * hd) // hd, hd)
+    value = value_full[:, :hkv]  # row stride value_row_stride when given (packed-qkv view)
+    slots = torch.randperm(num_blocks * block_size, generator=gen)[:n_tokens].to(torch.int32)
+    skip_pos = torch.randperm(n_tokens, generator=gen)[:skip]
+    slots[skip_pos] = -1
+    k_cache = torch.zeros(num_blocks, block_size, hkv, hd, dtype=torch.bfloat16)
+    v_cache = torch.zeros_like(k_cache)
+    return Case(dict(key=key, value=value, k_cache=k_cache, v_cache=v_cache, slot_mapping=slots),
+                dict(block_size=block_size, n_valid=n_tokens - skip))
+
+
+def _fill_pool(gen, pool_blocks, block_size, hkv, hd):
+    k_cache = _randn(gen, pool_blocks, block_size, hkv, hd)
+    v_cache = _randn(gen, pool_blocks, block_size, hkv, hd)
+    return k_cache, v_cache
+
+
+def decode_case(seed=1, batch=64, hq=HQ, hkv=HKV, hd=HD, block_size=BLOCK, ctx_lo=100,
+                ctx_hi=2048, pool_blocks=1024, ctx=None, width=None):
+    gen = torch.Generator().manual_seed(seed)
+    lens = list(ctx) if ctx is not None else _randint(gen, ctx_lo, ctx_hi, batch)
+    batch = len(lens)
+    perm = torch.randperm(pool_blocks, generator=gen).tolist()
+    tables, nxt = [], 0
+    for n in lens:
+        need = (n + block_size - 1) // block_size
+        tables.append(perm[nxt:nxt + need])
+        nxt += need
+    assert nxt <= pool_blocks, "pool too small"
+    q = _randn(gen, batch, hq, hd)
+    k_cache, v_cache = _fill_pool(gen, pool_blocks, block_size, hkv, hd)
+    bt = _pad_tables(tables, width)
+    return Case(dict(q=q, k_cache=k_cache, v_cache=v_cache, block_tables=bt,
+                     context_lens=torch.tensor(lens, dtype=torch.int32)),
+                dict(block_size=block_size, scale=hd ** -0.5, lens=lens, tables=tables))
+
+
+def _prefix_batch(gen, lens_new, cached, block_size, pool_blocks, shared_prefix_pages):
+    """Block tables for sequences with `cached[i]` cached tokens then `lens_new[i]` new ones.
+    The first `shared_prefix_pages` pages are common to every sequence."""
+    perm = torch.randperm(pool_blocks, generator=gen).tolist()
+    shared = perm[:shared_prefix_pages]
+    nxt = shared_prefix_pages
+    tables, slots = [], []
+    for n_new, c in zip(lens_new, cached):
+        total = c + n_new
+        need = (total + block_size - 1) // block_size
+        own = need - shared_prefix_pages
+        table = shared + perm[nxt:nxt + own]
+        nxt += own
+        tables.append(table)
+        for p in range(c, total):
+            slots.append(table[p // block_size] * block_size + p % block_size)
+    assert nxt <= pool_blocks, "pool too small"
+    return tables, slots
+
+
+def prefill_case(seed=2, nseq=32, prefix=512, new_lo=100, new_hi=1024, hq=HQ, hkv=HKV, hd=HD,
+                 block_size=BLOCK, pool_blocks=256, lens_new=None):
+    gen = torch.Generator().manual_seed(seed)
+    lens_new = list(lens_new) if lens_new is not None else _randint(gen, new_lo, new_hi, nseq)
+    nseq = len(lens_new)
+    assert prefix % block_size == 0
+    tables, slots = _prefix_batch(gen, lens_new, [prefix] * nseq, block_size, pool_blocks,
+                                  prefix // block_size)
+    tq = sum(lens_new)
+    q = _randn(gen, tq, hq, hd)
+    key = _randn(gen, tq, hkv, hd)
+    value = _randn(gen, tq, hkv, hd)
+    k_cache, v_cache = _fill_pool(gen, pool_blocks, block_size, hkv, hd)
+    cu_q = torch.tensor([0] + list(torch.tensor(lens_new).cumsum(0).tolist()), dtype=torch.int32)
+    lens_k = [prefix + n for n in lens_new]
+    cu_k = torch.tensor([0] + list(torch.tensor(lens_k).cumsum(0).tolist()), dtype=torch.int32)
+    return Case(dict(q=q, key=key, value=value, k_cache=k_cache, v_cache=v_cache,
+                     slot_mapping=torch.tensor(slots, dtype=torch.int32),
+                     block_tables=_pad_tables(tables), cu_seqlens_q=cu_q, cu_seqlens_k=cu_k),
+                dict(block_size=block_size, scale=hd ** -0.5, lens_q=lens_new, lens_k=lens_k,
+                     max_seqlen_q=max(lens_new), max_seqlen_k=max(lens_k), tables=tables))
+
+
+def spec_verify_case(seed=4, batch=32, n_query=6, n_draft=5, ctx_lo=1024, ctx_hi=8192, hq=HQ,
+                     hkv=HKV, hd=HD, block_size=BLOCK, pool_blocks=1100):
+    """The last `n_query` of each context are queries; the last `n_draft` of
+    those (the draft tokens) are stored in the step, the first query (the last
+    accepted token) is already cached."""
+    gen = torch.Generator().manual_seed(seed)
+    lens = _randint(gen, ctx_lo, ctx_hi, batch)
+    cached = [n - n_draft for n in lens]
+    tables, slots = _prefix_batch(gen, [n_draft] * batch, cached, block_size, pool_blocks, 0)
+    q = _randn(gen, batch * n_query, hq, hd)
+    key = _randn(gen, batch * n_draft, hkv, hd)
+    value = _randn(gen, batch * n_draft, hkv, hd)
+    k_cache, v_cache = _fill_pool(gen, pool_blocks, block_size, hkv, hd)
+    cu_q = torch.arange(0, (batch + 1) * n_query, n_query, dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32)
+    return Case(dict(q=q, key=key, value=value, k_cache=k_cache, v_cache=v_cache,
+                     slot_mapping=torch.tensor(slots, dtype=torch.int32),
+                     block_tables=_pad_tables(tables), cu_seqlens_q=cu_q, cu_seqlens_k=cu_k,
+                     context_lens=torch.tensor(lens, dtype=torch.int32)),
+                dict(block_size=block_size, scale=hd ** -0.5, lens_q=[n_query] * batch,
+                     lens_k=lens, max_seqlen_q=n_query, max_seqlen_k=max(lens), tables=tables))
+
+
+def mixed_layer_case(seed=3, n_chunks=8, chunk=512, cached_lo=0, cached_hi=1536, n_decode=192,
+                     ctx_lo=256, ctx_hi=4096, hq=HQ, hkv=HKV, hd=HD, block_size=BLOCK,
+                     pool_blocks=3300):
+    """One layer of a mixed step: prefill chunks (paged, mid-page starts allowed)
+    and decode sequences share one cache pool."""
+    gen = torch.Generator().manual_seed(seed)
+    cached = _randint(gen, cached_lo, cached_hi, n_chunks)
+    dec_lens = _randint(gen, ctx_lo, ctx_hi, n_decode)
+    perm = torch.randperm(pool_blocks, generator=gen).tolist()
+    nxt = 0
+    pf_tables, pf_slots = [], []
+    for c in cached:
+        total = c + chunk
+        need = (total + block_size - 1) // block_size
+        t = perm[nxt:nxt + need]
+        nxt += need
+        pf_tables.append(t)
+        for p in range(c, total):
+            pf_slots.append(t[p // block_size] * block_size + p % block_size)
+    dec_tables, dec_slots = [], []
+    for n in dec_lens:
+        need = (n + block_size - 1) // block_size
+        t = perm[nxt:nxt + need]
+        nxt += need
+        dec_tables.append(t)
+        dec_slots.append(t[(n - 1) // block_size] * block_size + (n - 1) % block_size)
+    assert nxt <= pool_blocks, "pool too small"
+    tq = n_chunks * chunk
+    q_pf = _randn(gen, tq, hq, hd)
+    q_dec = _randn(gen, n_decode, hq, hd)
+    key = _randn(gen, tq + n_decode, hkv, hd)
+    value = _randn(gen, tq + n_decode, hkv, hd)
+    k_cache, v_cache = _fill_pool(gen, pool_blocks, block_size, hkv, hd)
+    lens_k = [c + chunk for c in cached]
+    cu_q = torch.arange(0, (n_chunks + 1) * chunk, chunk, dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(torch.tensor(lens_k).cumsum(0).tolist()), dtype=torch.int32)
+    return Case(dict(q_prefill=q_pf, q_decode=q_dec, key=key, value=value, k_cache=k_cache,
+                     v_cache=v_cache,
+                     slot_mapping=torch.tensor(pf_slots + dec_slots, dtype=torch.int32),
+                     prefill_block_tables=_pad_tables(pf_tables), cu_seqlens_q=cu_q,
+                     cu_seqlens_k=cu_k, decode_block_tables=_pad_tables(dec_tables),
+                     context_lens=torch.tensor(dec_lens, dtype=torch.int32)),
+                dict(block_size=block_size, scale=hd ** -0.5, lens_q=[chunk] * n_chunks,
+                     lens_k=lens_k, max_seqlen_q=chunk, dec_lens=dec_lens))

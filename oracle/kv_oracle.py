@@ -1,0 +1,182 @@
+"""CPU oracle of the nano-vLLM KV-cache hot path.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py may import this module, and only as the checker
+or the timed CPU baseline.  The product (learn-nano-vllm_amd/nanovllm_amd and
+libnvk.so) never calls it: there is no CPU fallback.
+
+What it restates (numpy, bf16 carried as uint16 bit patterns):
+
+  kv_store          store_kvcache_kernel, nanovllm/layers/attention.py:10-30
+                    (k_cache.view(-1, D)[slot] = key[t], slot == -1 skipped)
+  paged_attention   flash_attn_varlen_func / flash_attn_with_kvcache as called
+                    at attention.py:64-74: per sequence, gather the keys through
+                    the block table (or take the dense rows), then
+                    softmax(scale * q k^T + M) v in float32, GQA kv head = h // G,
+                    M the bottom-right aligned causal mask (key j visible to
+                    query row i iff j <= i + Lk - Lq); rows that see no key are 0.
+  slots_for         the slot formula slot = bt[p // bs] * bs + p % bs used by
+                    model_runner.py:151-161, 181.
+
+How each function is pinned (tests/test_oracle.py):
+  kv_store          the guide's worked store example and test matrix
+                    (master_nano-vllm-v2.md:2807-2921) and a per-token
+                    brute-force loop; invariants (untouched cells, -1 rows, no
+                    K/V swap, inputs unmodified, store->gather round trip).
+  paged_attention   scalar brute force with math.exp on small cases, torch's
+                    CPU scaled_dot_product_attention where the two conventions
+                    coincide (Lq == Lk, and Lq == 1), closed forms (one key ->
+                    v; constant V -> V; q = 0 -> mean of the visible V rows,
+                    which fixes the causal alignment), block-table permutation
+                    invariance and the committed golden fixtures.  A planted
+                    mistake (top-left mask, h % Hkv head map, missing scale,
+                    off-by-one limit) fails at least one of these checks.
+  slots_for         the guide's known answer [14,15,0,3,20,21]
+                    (master_nano-vllm-v2.md:2766-2776).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = ["bf16_to_f32", "f32_to_bf16", "kv_store", "slots_for", "gather_rows",
+           "paged_attention", "attention_bytes", "prefill_flops"]
+
+
+# ---------------------------------------------------------------------------
+# bf16 helpers (bf16 = upper 16 bits of an IEEE float32)
+# ---------------------------------------------------------------------------
+def bf16_to_f32(u16: np.ndarray) -> np.ndarray:
+    return (np.asarray(u16, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even float32 -> bf16 bits (NaN kept quiet)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    out = rounded.astype(np.uint16)
+    nan = np.isnan(x)
+    out[nan] = 0x7FC0
+    return out
+
+
+# ---------------------------------------------------------------------------
+# KV-store scatter
+# ---------------------------------------------------------------------------
+def kv_store(key: np.ndarray, value: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+             slot_mapping: np.ndarray) -> None:
+    """In place: k_cache.reshape(-1, D)[slot] = key.reshape(N, D)[t] for slot != -1.
+
+    attention.py:21-30: one program per token, ``if slot == -1: return``, then a
+    contiguous D-element copy to ``slot * D``.  key/value: [N, ...] (any row
+    shape of D elements); caches: any shape whose trailing dims hold D per slot.
+    """
+    n = key.shape[0]
+    slots = np.asarray(slot_mapping).astype(np.int64).reshape(-1)
+    assert slots.shape[0] == n
+    d = int(np.prod(key.shape[1:])) if key.ndim > 1 else 1
+    kc = k_cache.reshape(-1, d)
+    vc = v_cache.reshape(-1, d)
+    valid = slots != -1
+    if np.any(slots[valid] < 0) or np.any(slots[valid] >= kc.shape[0]):
+        raise ValueError("slot outside the cache (undefined in the reference)")
+    kc[slots[valid]] = key.reshape(n, d)[valid]
+    vc[slots[valid]] = value.reshape(n, d)[valid]
+
+
+def slots_for(block_table, positions, block_size: int) -> list[int]:
+    """slot = block_table[p // bs] * bs + p % bs (model_runner.py:151-161, 181)."""
+    return [int(block_table[p // block_size]) * block_size + p % block_size for p in positions]
+
+
+def gather_rows(cache: np.ndarray, block_table, length: int, block_size: int) -> np.ndarray:
+    """Rows of one sequence's first ``length`` positions from a paged cache
+    [NB, bs, ...] (the guide's gather reference, master_nano-vllm-v2.md:2923-2944)."""
+    flat = cache.reshape(cache.shape[0] * cache.shape[1], *cache.shape[2:])
+    idx = np.asarray(slots_for(block_table, range(length), block_size), dtype=np.int64)
+    return flat[idx]
+
+
+# ---------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------
+def _attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, diag: int,
+            _mutation: str | None) -> np.ndarray:
+    """One sequence.  q [Lq, Hq, D], k/v [Lk, Hkv, D] float32 -> [Lq, Hq, D]."""
+    lq, hq, d = q.shape
+    lk, hkv = k.shape[0], k.shape[1]
+    g = hq // hkv
+    out = np.zeros((lq, hq, d), dtype=np.float32)
+    if lq == 0 or lk == 0:
+        return out
+    i = np.arange(lq)[:, None]
+    j = np.arange(lk)[None, :]
+    if _mutation == "top_left":
+        visible = j <= i
+    elif _mutation == "strict":
+        visible = j < i + diag
+    else:
+        visible = j <= i + diag                     # bottom-right aligned causal
+    eff_scale = 1.0 if _mutation == "no_scale" else scale
+    for h in range(hq):
+        kvh = h % hkv if _mutation == "gqa_mod" else h // g
+        s = (q[:, h, :] @ k[:, kvh, :].T) * np.float32(eff_scale)      # [Lq, Lk]
+        s = np.where(visible, s, -np.inf)
+        m = s.max(axis=1, keepdims=True)
+        has = np.isfinite(m[:, 0])
+        p = np.exp(s - np.where(np.isfinite(m), m, 0.0))
+        l = p.sum(axis=1, keepdims=True)
+        o = (p @ v[:, kvh, :]) / np.where(l > 0, l, 1.0)
+        out[:, h, :] = np.where(has[:, None], o, 0.0)
+    return out
+
+
+def paged_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_seqlens_q, seqlens_k,
+                    scale: float, block_tables: np.ndarray | None = None, block_size: int = 0,
+                    cu_seqlens_k=None, _mutation: str | None = None) -> np.ndarray:
+    """Varlen causal attention, float32.
+
+    q: [Tq, Hq, D] float32.  Sequence s owns query rows cu_seqlens_q[s]:cu_seqlens_q[s+1]
+    and has seqlens_k[s] keys.  Paged (block_tables given): k/v are caches
+    [NB, bs, Hkv, D] and key p of sequence s is at page block_tables[s][p // bs].
+    Dense: k/v are [Tk, Hkv, D] and sequence s's keys are rows
+    cu_seqlens_k[s]:cu_seqlens_k[s+1].  Decode is the case Lq == 1.
+    ``_mutation`` plants a known mistake; only the oracle's own tests use it.
+    """
+    cu_q = np.asarray(cu_seqlens_q, dtype=np.int64)
+    lens_k = np.asarray(seqlens_k, dtype=np.int64)
+    out = np.zeros(q.shape, dtype=np.float32)
+    for s in range(cu_q.shape[0] - 1):
+        q0, q1 = int(cu_q[s]), int(cu_q[s + 1])
+        lk = int(lens_k[s])
+        if block_tables is not None:
+            ks = gather_rows(k, block_tables[s], lk, block_size)
+            vs = gather_rows(v, block_tables[s], lk, block_size)
+        else:
+            k0 = int(cu_seqlens_k[s])
+            ks, vs = k[k0:k0 + lk], v[k0:k0 + lk]
+        lq = q1 - q0
+        out[q0:q1] = _attend(q[q0:q1].astype(np.float32), ks.astype(np.float32),
+                             vs.astype(np.float32), scale, lk - lq, _mutation)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Algorithmic work counts (roofline numerators)
+# ---------------------------------------------------------------------------
+def attention_bytes(seqlens_k, num_kv_heads: int, head_dim: int, n_q_rows: int, num_q_heads: int,
+                    elem_bytes: int = 2) -> int:
+    """Unique K+V bytes of every sequence's keys + q read + out written."""
+    kv = 2 * int(np.sum(np.asarray(seqlens_k, dtype=np.int64))) * num_kv_heads * head_dim * elem_bytes
+    return kv + 2 * n_q_rows * num_q_heads * head_dim * elem_bytes
+
+
+def prefill_flops(seqlens_q, seqlens_k, num_q_heads: int, head_dim: int) -> int:
+    """4 * Hq * D * (number of unmasked (query, key) pairs): QK^T plus PV."""
+    pairs = 0
+    for lq, lk in zip(seqlens_q, seqlens_k):
+        lq, lk = int(lq), int(lk)
+        diag = lk - lq
+        for i in range(lq):
+            pairs += max(0, min(lk, i + diag + 1))
+    return 4 * num_q_heads * head_dim * pairs

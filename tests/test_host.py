@@ -1,0 +1,156 @@
+"""CPU tests of the host side: the C-ABI library surface, argument validation
+(no kernel launch), the Context record and the metadata builders."""
+import dataclasses
+import json
+import os
+import re
+
+import pytest
+import torch
+
+from nanovllm_amd import _lib
+from nanovllm_amd.engine import metadata
+from nanovllm_amd.engine.sequence import Sequence
+from nanovllm_amd.utils import context as ctx_mod
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nvk.h")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nvk_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    names = header_functions()
+    assert {"nvk_kv_store", "nvk_paged_decode", "nvk_varlen_prefill"} <= set(names)
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with nvk.h"
+    assert lib.nvk_build_target() == b"gfx950"
+
+
+@pytest.mark.skipif(torch.cuda.is_available(),
+                    reason="passes fake device pointers; a validation regression must not be "
+                           "able to launch a kernel on them, so it only runs without a GPU")
+def test_error_codes_without_launching():
+    lib = _lib.load()
+    assert lib.nvk_strerror(0) == b"ok"
+    for code in (-1, -2, -3, -4):
+        assert lib.nvk_strerror(code).startswith(b"nvk:")
+    # unsupported element size / negative count / zero tokens (nothing launched)
+    assert lib.nvk_kv_store(1, 8, 1, 8, 1, 1, 1, 4, 8, 3, 100, None) == -2
+    assert lib.nvk_kv_store(1, 8, 1, 8, 1, 1, 1, -1, 8, 2, 100, None) == -1
+    assert lib.nvk_kv_store(None, 8, None, 8, None, None, None, 0, 8, 2, 100, None) == 0
+    # decode: fp16 not built, head_dim 96 not built, G=3 not built, bad scale
+    args = [16, 16 * 128, 128, 16, 16, 16, 8, 16, 4, 16, 8, 128, 256, 8, 1024, 0.088, 16, 16 * 128,
+            128, 16, 1 << 30]
+    assert lib.nvk_paged_decode(*args, 1, None) == -2
+    bad_hd = list(args); bad_hd[11] = 96
+    assert lib.nvk_paged_decode(*bad_hd, 0, None) == -2
+    bad_g = list(args); bad_g[9] = 12; bad_g[10] = 4
+    assert lib.nvk_paged_decode(*bad_g, 0, None) == -2
+    bad_scale = list(args); bad_scale[15] = 0.0
+    assert lib.nvk_paged_decode(*bad_scale, 0, None) == -1
+    # workspace too small
+    small_ws = list(args); small_ws[20] = 16
+    assert lib.nvk_paged_decode(*small_ws, 0, None) == -4
+    assert lib.nvk_paged_decode_workspace_size(64, 16, 128, 256, 8) == 64 * 16 * 8 * (128 + 2) * 4
+    assert lib.nvk_paged_decode_workspace_size(4, 16, 128, 256, 1) == 0
+    # prefill: head_dim 64 not built
+    assert lib.nvk_varlen_prefill(16, 2048, 128, 4, 16, 16, 1024, 1024, 128, 4, 16, 16, 1, 4, None,
+                                  0, 0, 0, 0, 16, 8, 64, 0.1, 16, 2048, 128, 0, None) == -2
+
+
+def test_cpu_tensors_are_rejected_not_served():
+    k = torch.zeros(2, 1, 8, dtype=torch.bfloat16)
+    kc = torch.zeros(1, 4, 1, 8, dtype=torch.bfloat16)
+    with pytest.raises(_lib.NvkError):
+        ctx_mod.set_context(False)
+        from nanovllm_amd import store_kvcache
+        store_kvcache(k, k, kc, kc.clone(), torch.tensor([0, 1], dtype=torch.int32))
+
+
+def test_context_record_matches_reference_fields():
+    fields = [(f.name, f.default) for f in dataclasses.fields(ctx_mod.Context)]
+    assert fields == [("is_prefill", False), ("cu_seqlens_q", None), ("cu_seqlens_k", None),
+                      ("max_seqlen_q", 0), ("max_seqlen_k", 0), ("slot_mapping", None),
+                      ("context_lens", None), ("block_tables", None)]
+    ctx_mod.set_context(True, max_seqlen_q=3)
+    assert ctx_mod.get_context().is_prefill and ctx_mod.get_context().max_seqlen_q == 3
+    ctx_mod.reset_context()
+    assert ctx_mod.get_context() == ctx_mod.Context()
+
+
+def _known():
+    with open(os.path.join(GOLDEN, "guide_known_answers.json")) as f:
+        return json.load(f)
+
+
+def test_prefill_slots_reproduce_guide_example():
+    ex = _known()["slot_example"]
+    bs = ex["block_size"]
+    seq = Sequence(list(range(12)), block_table=ex["block_table"], num_cached_tokens=2,
+                   num_scheduled_tokens=8)
+    slots = metadata.prefill_slots(seq, bs)
+    by_pos = dict(zip(range(2, 10), slots))
+    assert [by_pos[p] for p in ex["positions"]] == ex["slots"]
+
+
+def test_prepare_prefill_lm_head_example_and_no_prefix():
+    ex = _known()["lm_head_example"]
+    seqs = []
+    nxt = 0
+    for n in ex["query_lens"]:
+        seqs.append(Sequence(list(range(n)), block_table=[nxt], num_scheduled_tokens=n))
+        nxt += 1
+    metadata.prepare_prefill(seqs, 256, device="cpu")
+    c = ctx_mod.get_context()
+    assert c.cu_seqlens_q.tolist() == ex["cu_seqlens_q"]
+    assert (c.cu_seqlens_q[1:] - 1).tolist() == ex["last_indices"]
+    assert c.block_tables is None                       # nothing cached
+    assert c.cu_seqlens_q.dtype == torch.int32 and c.slot_mapping.dtype == torch.int32
+    assert c.slot_mapping.tolist() == [0, 1, 256, 512, 513, 514, 515]
+
+
+def test_prepare_prefill_chunk_with_prefix_and_warmup():
+    bs = 4
+    a = Sequence(list(range(10)), block_table=[7, 2, 9], num_cached_tokens=4,
+                 num_scheduled_tokens=5)               # chunk of 5 after a cached page
+    warm = Sequence([0] * 3, num_scheduled_tokens=3)    # warmup: no block table, no slots
+    warm.block_table = []
+    metadata.prepare_prefill([a, warm], bs, device="cpu")
+    c = ctx_mod.get_context()
+    assert c.cu_seqlens_q.tolist() == [0, 5, 8]
+    assert c.cu_seqlens_k.tolist() == [0, 9, 12]
+    assert c.max_seqlen_q == 5 and c.max_seqlen_k == 9
+    assert c.slot_mapping.tolist() == [8, 9, 10, 11, 36]
+    assert c.block_tables.tolist() == [[7, 2, 9], [-1, -1, -1]]
+
+
+def test_prepare_decode_slot_and_context_lens(monkeypatch):
+    bs = 4
+    monkeypatch.setattr(Sequence, "block_size", bs)       # as LLMEngine does (llm_engine.py:21)
+    a = Sequence(list(range(9)), block_table=[3, 0, 5])   # 9 tokens: last in page 5 offset 0
+    b = Sequence(list(range(4)), block_table=[1])
+    metadata.prepare_decode([a, b], bs, device="cpu")
+    c = ctx_mod.get_context()
+    assert c.slot_mapping.tolist() == [20, 7]
+    assert c.context_lens.tolist() == [9, 4]
+    assert c.block_tables.tolist() == [[3, 0, 5], [1, -1, -1]]
+    assert not c.is_prefill
+
+
+def test_graph_buffers_pad_rows_like_run_model():
+    g = metadata.DecodeGraphBuffers(8, 4, device="cpu")
+    g.block_tables.fill_(77)                            # stale content from an earlier step
+    g.load(torch.tensor([5, 9], dtype=torch.int32), torch.tensor([6, 10], dtype=torch.int32),
+           torch.tensor([[1, -1], [2, 3]], dtype=torch.int32))
+    assert g.slot_mapping.tolist() == [5, 9] + [-1] * 6
+    assert g.context_lens.tolist() == [6, 10] + [0] * 6
+    assert g.block_tables[:2].tolist() == [[1, -1, 77, 77], [2, 3, 77, 77]]
+    assert g.block_tables[2:].eq(77).all()
