@@ -1,0 +1,253 @@
+#!/usr/bin/env python3
+"""Benchmark of the nano-vLLM KV-cache hot path on one MI355X.
+
+Headline (`value`): paged GQA decode attention, Qwen3-0.6B shape: batch 64,
+16 q / 8 kv heads, head_dim 128, bf16, 256-token pages, context U{100..2048}
+(seeded).  A step is one decode-attention call over the batch (the split-K
+kernel and its combine pass).  `value` = algorithmic bytes of a step (unique
+K+V bytes of every context + q read + output written) / wall time per step,
+with every input resident in HBM.  Two more legs ride along in the same JSON
+line: the KV-store scatter (4096 tokens into a 64-page cache, 5 % slots -1)
+in GB/s and the varlen prefill over a 512-token shared prefix (32 sequences,
+U{100..1024} new tokens) in TFLOP/s of unmasked QK^T + PV work.
+
+Timing: each leg builds K steps into one HIP graph (the decode steps cycle
+over four copies of the KV pool, so no step finds its working set in the
+256 MB Infinity Cache), replays it W-step-graph first as warmup, then
+brackets one replay of the K-step graph with device synchronisation (wall
+clock -> ms_per_step) and HIP events on the launch stream (-> roofline
+achieved).  The CPU baseline is the numpy oracle on one host thread, timed on
+the same inputs.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "learn-nano-vllm_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+METRIC = "decode-attn + KV-store HBM GB/s (% peak); prefill MFMA util; Qwen3-0.6B shape"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--legs", default="decode,store,prefill",
+                   help="comma list of legs to run (decode is the headline)")
+    return p.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_graph(torch, step_fns, steps, warmup):
+    """Capture `steps` calls (cycling over step_fns) in one graph; return
+    (wall seconds per step, event seconds per step)."""
+    def capture(n):
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(len(step_fns)):          # eager warmup of every variant
+                step_fns[i]()
+        torch.cuda.current_stream().wait_stream(s)
+        with torch.cuda.graph(g):
+            for i in range(n):
+                step_fns[i % len(step_fns)]()
+        return g
+
+    g_warm = capture(max(1, warmup))
+    g = capture(steps)
+    g_warm.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    ev = start.elapsed_time(end) / 1e3 / steps
+    return wall, ev
+
+
+def cpu_time(fn, reps):
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def traffic_for(leg):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f).get(leg, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: the KV-cache path runs on a single MI355X "
+              "(no sharding is built); run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    from nanovllm_amd import paged_decode, store_kvcache, varlen_prefill
+    from nanovllm_amd.workloads import decode_case, kv_store_case, prefill_case
+    from oracle import kv_oracle as orc
+
+    legs = set(args.legs.split(","))
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    result = {}
+
+    # ------------------------------------------------------------------ decode
+    log("building decode workload (B=64, ctx U{100..2048}, 1024-page pool)")
+    dc = decode_case()
+    pools = [dc.to(dev)] + [dc.to(dev) for _ in range(3)]   # four separate copies
+    outs = [torch.empty(64, 16, 128, dtype=torch.bfloat16, device=dev) for _ in pools]
+    dec_fns = [
+        (lambda c=c, o=o: paged_decode(c.q, c.k_cache, c.v_cache, c.context_lens,
+                                       c.block_tables, dc.scale, out=o))
+        for c, o in zip(pools, outs)]
+    dec_bytes = orc.attention_bytes(dc.lens, 8, 128, 64, 16)
+    log("timing decode")
+    wall, ev = time_graph(torch, dec_fns, args.steps, args.warmup)
+    dec_gbs = dec_bytes / wall / 1e9
+    dec_ach = dec_bytes / ev / 1e9
+    result["decode"] = dict(ms_per_step=wall * 1e3, gbs=dec_gbs, event_gbs=dec_ach,
+                            bytes_per_step=dec_bytes)
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline: decode oracle, 1 thread")
+        q, kc, vc = bits(dc.q), bits(dc.k_cache), bits(dc.v_cache)
+        lens, bt = dc.context_lens.numpy(), dc.block_tables.numpy()
+        with threadpool_limits(1):
+            t = cpu_time(lambda: orc.paged_attention(q, kc, vc, np.arange(65), lens, dc.scale,
+                                                     block_tables=bt, block_size=256), 20)
+        cpu = {"value": round(dec_bytes / t / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": "the full 64-sequence decode batch through the numpy oracle "
+                         "(gather + f32 softmax attention), median of 20 reps on 1 host thread"}
+    del pools, outs, dec_fns
+
+    # ------------------------------------------------------------------ store
+    if "store" in legs:
+        log("building kv-store workload (4096 tokens, 64 pages, 205 slots -1)")
+        sc = kv_store_case()
+        copies = [sc.to(dev) for _ in range(4)]
+        st_fns = [(lambda c=c: store_kvcache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping))
+                  for c in copies]
+        n_valid = int((sc.slot_mapping >= 0).sum())
+        st_bytes = n_valid * 2 * 2 * 8 * 128 * 2 + 4 * 4096
+        log("timing kv-store")
+        wall_s, ev_s = time_graph(torch, st_fns, args.steps, args.warmup)
+        leg = dict(ms_per_step=wall_s * 1e3, bytes_per_step=st_bytes,
+                   roofline={"bound": "hbm", "achieved": round(st_bytes / ev_s / 1e9, 2),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(st_bytes / ev_s / 1e9 / HBM_PEAK_GBS, 4),
+                             "traffic": traffic_for("kv_store")})
+        if not args.no_cpu_baseline:
+            kb, vb, sl = bits(sc.key), bits(sc.value), sc.slot_mapping.numpy()
+            kc0, vc0 = bits(sc.k_cache), bits(sc.v_cache)
+
+            def cpu_store():
+                kc, vc = kc0.copy(), vc0.copy()
+                orc.kv_store(kb, vb, kc, vc, sl)
+            t = cpu_time(cpu_store, 50)
+            leg["cpu_baseline"] = {"value": round(st_bytes / t / 1e9, 3), "unit": "GB/s",
+                                   "cores": 1, "kind": "port",
+                                   "sample": "full 4096-token store via numpy index assignment "
+                                             "(cache copy included), median of 50 reps"}
+        result["kv_store"] = leg
+        del copies, st_fns
+
+    # ------------------------------------------------------------------ prefill
+    if "prefill" in legs:
+        log("building prefill workload (32 seqs, 512-token shared prefix)")
+        pc = prefill_case()
+        copies = [pc.to(dev) for _ in range(2)]
+        for c in copies:   # the new tokens' K/V are in the cache before attention
+            store_kvcache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping)
+        outs = [torch.empty_like(c.q) for c in copies]
+        pf_fns = [(lambda c=c, o=o: varlen_prefill(c.q, c.k_cache, c.v_cache, c.cu_seqlens_q,
+                                                   c.cu_seqlens_k, pc.max_seqlen_q, pc.scale,
+                                                   block_table=c.block_tables, out=o))
+                  for c, o in zip(copies, outs)]
+        flops = orc.prefill_flops(pc.lens_q, pc.lens_k, 16, 128)
+        log("timing prefill")
+        wall_p, ev_p = time_graph(torch, pf_fns, args.steps, args.warmup)
+        tf = flops / ev_p / 1e12
+        leg = dict(ms_per_step=wall_p * 1e3, flops_per_step=flops,
+                   roofline={"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                             "traffic": traffic_for("prefill")})
+        if not args.no_cpu_baseline:
+            kc, vc = bits(pc.k_cache).copy(), bits(pc.v_cache).copy()
+            orc.kv_store(bits(pc.key), bits(pc.value), kc, vc, pc.slot_mapping.numpy())
+            qb, cuq, bt = bits(pc.q), pc.cu_seqlens_q.numpy(), pc.block_tables.numpy()
+            with threadpool_limits(1):
+                t = cpu_time(lambda: orc.paged_attention(qb, kc, vc, cuq, pc.lens_k, pc.scale,
+                                                         block_tables=bt, block_size=256), 3)
+            leg["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
+                                   "cores": 1, "kind": "port",
+                                   "sample": "the full 32-sequence prefill through the numpy "
+                                             "oracle, median of 3 reps on 1 host thread"}
+        result["prefill"] = leg
+
+    d = result["decode"]
+    line = {
+        "metric": METRIC,
+        "value": round(d["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(d["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "paged GQA decode attention: batch 64, 16 q / 8 kv heads, "
+                               "head_dim 128, bf16, 256-token pages, context U{100..2048} (seed 1)",
+                   "batch": 64, "num_q_heads": 16, "num_kv_heads": 8, "head_dim": 128,
+                   "block_size": 256, "context": "U{100..2048}",
+                   "bytes_per_step": d["bytes_per_step"]},
+        "roofline": {"bound": "hbm", "achieved": round(d["event_gbs"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(d["event_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_for("decode")},
+        "cpu_baseline": cpu,
+    }
+    for k in ("kv_store", "prefill"):
+        if k in result:
+            line[k] = result[k]
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -131,12 +131,19 @@ def _attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, diag: int
     return out
 
 
+def _as_f32(x: np.ndarray) -> np.ndarray:
+    """float arrays as float32; uint16 arrays are bf16 bit patterns."""
+    return bf16_to_f32(x) if x.dtype == np.uint16 else x.astype(np.float32)
+
+
 def paged_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_seqlens_q, seqlens_k,
                     scale: float, block_tables: np.ndarray | None = None, block_size: int = 0,
                     cu_seqlens_k=None, _mutation: str | None = None) -> np.ndarray:
     """Varlen causal attention, float32.
 
-    q: [Tq, Hq, D] float32.  Sequence s owns query rows cu_seqlens_q[s]:cu_seqlens_q[s+1]
+    q, k, v: float arrays, or uint16 arrays holding bf16 bit patterns (only the
+    rows a sequence reads are widened).
+    q: [Tq, Hq, D].  Sequence s owns query rows cu_seqlens_q[s]:cu_seqlens_q[s+1]
     and has seqlens_k[s] keys.  Paged (block_tables given): k/v are caches
     [NB, bs, Hkv, D] and key p of sequence s is at page block_tables[s][p // bs].
     Dense: k/v are [Tk, Hkv, D] and sequence s's keys are rows
@@ -156,8 +163,8 @@ def paged_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_seqlens_q, s
             k0 = int(cu_seqlens_k[s])
             ks, vs = k[k0:k0 + lk], v[k0:k0 + lk]
         lq = q1 - q0
-        out[q0:q1] = _attend(q[q0:q1].astype(np.float32), ks.astype(np.float32),
-                             vs.astype(np.float32), scale, lk - lq, _mutation)
+        out[q0:q1] = _attend(_as_f32(q[q0:q1]), _as_f32(ks), _as_f32(vs), scale, lk - lq,
+                             _mutation)
     return out
 
 
