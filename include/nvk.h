@@ -106,10 +106,14 @@ int nvk_kv_store(const void* key, int64_t key_row_stride,
  *   (model_runner.py:180).  context_lens[b] == 0 (a padded graph row) writes
  *   zeros.  Lengths above max_blocks*block_size are clamped to it; page ids
  *   outside [0, num_blocks) contribute no keys.
- * workspace: device scratch of nvk_paged_decode_workspace_size() bytes
- *   (split-K partial results); it need not be initialised.
+ * workspace: device scratch of nvk_paged_decode_workspace_size() bytes, 256-byte
+ *   aligned (per-context descriptors and the partial results of contexts split
+ *   between waves); it need not be initialised, every call writes what it
+ *   reads.  Two calls in flight at once need two workspaces.
+ * Two kernels are enqueued: the balanced split-K pass and a combine pass.
  * scale must be > 0.  dtype: NVK_DTYPE_BF16.  head_dim: 128 or 64.
- * G: 1, 2, 4 or 8.
+ * G: 1, 2, 4 or 8.  batch <= 2048.  q, k_cache, v_cache and out 16-byte
+ * aligned, token / head strides multiples of 8 elements.
  */
 int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                      const void* k_cache, const void* v_cache,
@@ -124,8 +128,8 @@ int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
 
 /* Bytes of workspace nvk_paged_decode needs for these sizes (0 on bad input). */
 size_t nvk_paged_decode_workspace_size(int32_t batch, int32_t num_q_heads,
-                                       int32_t head_dim, int32_t block_size,
-                                       int32_t max_blocks);
+                                       int32_t num_kv_heads, int32_t head_dim,
+                                       int32_t block_size, int32_t max_blocks);
 
 /*
  * Varlen causal attention over new tokens, with or without a paged prefix.

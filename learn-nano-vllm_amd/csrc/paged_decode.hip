@@ -6,27 +6,53 @@
 // first context_lens[b] cached keys of its sequence (causal is a no-op for a
 // single query row); q head h reads kv head h / (Hq/Hkv).
 //
-// Decomposition (split-K, "flash decoding"):
-//   grid = (splits, Hkv, B), split = SPLIT consecutive key positions
-//   (256 = one page at the reference's block size).  A workgroup owns one
-//   (sequence, kv head, split) and all G = Hq/Hkv query heads of that kv
-//   head, so each K/V byte is read from HBM once per step.  Its 4 waves each
-//   stream 64 keys: the K row of a key (HD bf16 = 256 B for HD=128) is spread
-//   over HD/8 lanes with one 16-byte load each, so one load instruction covers
-//   64/(HD/8) whole rows and a wave keeps 2*64*HD*2 bytes (32 KiB) in flight.
-//   q.k is v_dot2_f32_bf16 on bf16 pairs followed by a DPP butterfly over the
-//   HD/8 lanes of the row; P.V packs two keys' probabilities as a bf16 pair and
-//   uses v_dot2_f32_bf16 against the two keys' V values (f32 accumulation).
-//   The online-softmax state (m, l, o) is merged across the 4 waves in LDS,
-//   then either written as the final bf16 row (single split) or as an f32
-//   partial that a second kernel combines.
+// The step is a pure HBM stream (2 FLOP per byte), so the design is about
+// keeping the memory system busy with useful bytes only.
+//
+// Lane mapping.  A token's K (or V) row in the cache is Hkv*HD contiguous
+// bf16 (2 KiB for Qwen3-0.6B).  A wave's 16-byte-per-lane load instruction
+// covers 1 KiB = 64/(HD/8) head rows: HPI consecutive kv heads of the same
+// token times 64/(HD/8)/HPI tokens.  The mapping supports any power-of-two
+// HPI; the library uses HPI = 1 (4 tokens x one head's 256 B for HD = 128, see
+// decode_hpi).  Each group of HD/8 lanes ("row group") sees one kv head and
+// keeps the online-softmax state (m, l, o) of the G query heads that read it;
+// row groups of the same head are merged when a group of work ends.  q.k is
+// v_dot2_f32_bf16 on bf16 pairs plus a DPP butterfly over the row group; P.V
+// packs two keys' probabilities as bf16x2 and applies v_dot2_f32_bf16 against
+// the two keys' V values, f32 accumulation.
+//
+// Work split: balanced stream-K.  A group is (sequence b, block of HPI kv
+// heads); its keys are cut into chunks of TC = 8 * (tokens per instruction)
+// tokens, i.e. 8 load instructions of K and 8 of V (16 KiB per wave).  Groups
+// are ordered b-major, head block next, and the T chunks of the step are cut
+// into equal contiguous ranges, one per wave of a persistent grid of at most
+// 512 workgroups x 4 waves (static, so the launch can be captured in a graph;
+// when T is small only T/8 waves take part).  Every wave streams the same
+// number of bytes whatever the mix of context lengths.  Measured on MI355X, a
+// wave that issues one chunk, waits and computes it, with 8 waves per CU,
+// streams this access pattern at the rate of a plain read probe; deeper
+// per-wave prefetch or more waves only add cache pressure.  K/V loads are
+// non-temporal (read once).  The page of a chunk comes through a scalar load
+// when a page holds whole chunks.
+//
+// Finishing: a group that ends inside a wave's range is normalised in
+// registers and written as bf16.  A group cut between waves leaves one
+// partial (o, m, l) record per wave and head; every wave also writes the
+// group's descriptor (its first and last wave), so a small combine kernel
+// merges the cut groups after two dependent reads and writes the zero rows of
+// empty contexts.  (Merging inside the main kernel needs cross-XCD release /
+// acquire fences per part; on MI355X those cost far more than the combine.)
 #include "nvk_common.h"
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kTile = 64;                  // keys per wave per tile
-constexpr int kSplit = kWaves * kTile;     // keys per workgroup (one split)
+constexpr int kLoads = 8;          // load instructions per tensor per chunk
+constexpr int kWavesPerWG = 4;
+constexpr int kMaxWGs = 512;       // 256 CUs x 2 workgroups (8 waves per CU)
+constexpr int kMaxBatch = 2048;    // sequences per call (LDS prefix table)
+constexpr int kMinChunks = 8;      // a wave streams at least this many chunks
+
+typedef __attribute__((address_space(4))) const int32_t nvk_const_i32;
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -41,287 +67,485 @@ struct DecodeArgs {
   float scale_log2;  // softmax_scale * log2(e)
   uint16_t* out;
   int64_t out_stride_tok, out_stride_head;
-  float* ws_o;   // [B][Hq][S][HD]
-  float* ws_ml;  // [B][Hq][S][2]
-  int max_splits;
+  int32_t* ws_desc;  // [batch][Hkv/HPI] x 2: first and last wave of the group, -1 if empty
+  float* ws_rec;     // [P][2][HPI][G][HD+4] partial records
+  int n_waves;       // P: waves of the grid
+  int hpi;           // kv heads per load instruction
+  int tc;            // tokens per chunk
 };
 
+// context_lens and block_tables are read-only for the whole launch: read them
+// through the constant address space so wave-uniform reads become scalar loads.
 __device__ __forceinline__ int clamp_ctx(const DecodeArgs& a, int b) {
-  int ctx = a.context_lens[b];
+  int ctx = ((nvk_const_i32*)a.context_lens)[b];
   const int64_t cap = (int64_t)a.max_blocks * a.block_size;
   if (ctx < 0) ctx = 0;
   if ((int64_t)ctx > cap) ctx = (int)cap;
   return ctx;
 }
 
-template <int HD>
-__device__ __forceinline__ float group_sum_row(float x) {
-  return nvk_group_sum<HD / 8>(x);
+// Waves that take part for T chunks: at most P, and few enough that each
+// range holds kMinChunks chunks (bounds how finely a context is split).
+__device__ __forceinline__ int64_t active_waves(int64_t T, int64_t P) {
+  int64_t p = T / kMinChunks;
+  if (p > P) p = P;
+  return p < 1 ? 1 : p;
+}
+// first chunk of wave w's range
+__device__ __forceinline__ int64_t range_begin(int64_t w, int64_t T, int64_t P) { return w * T / P; }
+// wave whose range holds chunk c
+__device__ __forceinline__ int64_t chunk_owner(int64_t c, int64_t T, int64_t P) {
+  return ((c + 1) * P - 1) / T;
 }
 
-// max over the lanes that share the same position within a row (all lanes
-// whose index differs by a multiple of HD/8).
-template <int HD>
-__device__ __forceinline__ float cross_group_max(float x) {
-  if constexpr (HD == 64) x = fmaxf(x, nvk_dpp<0x128>(x));  // row_ror:8
-  x = fmaxf(x, nvk_xor_lane<16>(x));
-  x = fmaxf(x, nvk_xor_lane<32>(x));
-  return x;
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ float xor_lane(float x, int mask) {
+  const int lane = __lane_id();
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(x)));
 }
-template <int HD>
-__device__ __forceinline__ float cross_group_sum(float x) {
-  if constexpr (HD == 64) x += nvk_dpp<0x128>(x);
-  x += nvk_xor_lane<16>(x);
-  x += nvk_xor_lane<32>(x);
-  return x;
+
+// Exclusive prefix of chunks per sequence into s_cs[0..B]; returns the total.
+__device__ int chunk_prefix(const DecodeArgs& a, int* s_cs, int* s_wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int B = a.batch;
+  const int per = (B + 255) / 256;
+  const int b0 = tid * per;
+  int local = 0;
+  for (int i = 0; i < per; ++i) {
+    const int b = b0 + i;
+    if (b < B) local += (clamp_ctx(a, b) + a.tc - 1) / a.tc;
+  }
+  int x = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) s_wsum[wave] = x;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += s_wsum[w];
+  int run = base + x - local;
+  for (int i = 0; i < per; ++i) {
+    const int b = b0 + i;
+    if (b < B) {
+      s_cs[b] = run;
+      run += (clamp_ctx(a, b) + a.tc - 1) / a.tc;
+    }
+  }
+  const int total = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
+  if (tid == 0) s_cs[B] = total;
+  __syncthreads();
+  return total;
 }
+
+// Loads of one chunk held by one lane.
+template <int HD, int G>
+struct ChunkBuf {
+  static constexpr int LPR = HD / 8;   // lanes per head row
+  nvk_u32x4 k[kLoads], v[kLoads];
+  uint32_t q[G][4];
+};
+
+// Position of a wave in its range (all fields wave-uniform).
+struct ChunkPos {
+  int b, blk, k, n;  // sequence, kv-head block, chunk index in the group, chunks in the group
+};
+
+__device__ __forceinline__ void advance(ChunkPos& p, const int* s_cs, int n_blk) {
+  if (++p.k == p.n) {
+    p.k = 0;
+    if (++p.blk == n_blk) {
+      p.blk = 0;
+      int b = p.b + 1;
+      while (s_cs[b + 1] == s_cs[b]) ++b;  // skip empty contexts (a next chunk exists)
+      p.b = b;
+      p.n = s_cs[b + 1] - s_cs[b];
+    }
+  }
+  p.b = uniform(p.b); p.blk = uniform(p.blk); p.k = uniform(p.k); p.n = uniform(p.n);
+}
+
+// This lane's place in a load instruction.
+struct LaneRole {
+  int j;    // 16-byte chunk of the head row: d in [8j, 8j+8)
+  int hh;   // kv head within the block
+  int tt;   // token within the instruction
+};
+
+// Issues the loads of chunk p.  Every lane issues the same load instructions
+// whatever the data (no branches).  A row that does not exist (past the
+// context, or a page id outside the pool) reads this lane's q row instead: it
+// is finite, and its probability is masked to exactly 0 by the scores.
+template <int HD, int G, bool ALIGNED>
+__device__ __forceinline__ void load_chunk(const DecodeArgs& a, const ChunkPos& p, int ctx,
+                                           const LaneRole& r, int tpi, ChunkBuf<HD, G>& buf) {
+  const int64_t row_elems = (int64_t)a.num_kv_heads * HD;
+  const int kvh = p.blk * a.hpi + r.hh;
+  const int64_t head_off = (int64_t)kvh * HD + 8 * r.j;
+  const int base = p.k * a.tc;  // < ctx: p is a chunk of the group
+  const uint16_t* q0 = a.q + (int64_t)p.b * a.q_stride_tok +
+                       (int64_t)(kvh * G) * a.q_stride_head + 8 * r.j;
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const nvk_u32x4 v = *reinterpret_cast<const nvk_u32x4*>(q0 + h * a.q_stride_head);
+    buf.q[h][0] = v.x; buf.q[h][1] = v.y; buf.q[h][2] = v.z; buf.q[h][3] = v.w;
+  }
+  const int64_t bt_off = (int64_t)p.b * a.bt_stride;
+  if constexpr (ALIGNED) {
+    // the whole chunk lies in one page: one scalar table read
+    const int logical = a.bs_shift >= 0 ? (base >> a.bs_shift) : base / a.block_size;
+    const int page = ((nvk_const_i32*)a.block_tables)[bt_off + logical];
+    const bool page_ok = page >= 0 && page < a.num_blocks;
+    const int64_t row0 = (int64_t)page * a.block_size + (base - logical * a.block_size);
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int t = i * tpi + r.tt;
+      const bool ok = page_ok && base + t < ctx;
+      const int64_t off = (row0 + t) * row_elems + head_off;
+      const uint16_t* kp = ok ? a.k_cache + off : q0;
+      const uint16_t* vp = ok ? a.v_cache + off : q0;
+      buf.k[i] = __builtin_nontemporal_load(reinterpret_cast<const nvk_u32x4*>(kp));
+      buf.v[i] = __builtin_nontemporal_load(reinterpret_cast<const nvk_u32x4*>(vp));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int pos = base + i * tpi + r.tt;
+      const int lpos = pos < ctx ? pos : ctx - 1;  // keeps the table read inside the row
+      const int64_t row = nvk_paged_row(a.block_tables + bt_off, lpos, a.block_size, a.bs_shift,
+                                        a.num_blocks);
+      const bool ok = pos < ctx && row >= 0;
+      const int64_t off = row * row_elems + head_off;
+      const uint16_t* kp = ok ? a.k_cache + off : q0;
+      const uint16_t* vp = ok ? a.v_cache + off : q0;
+      buf.k[i] = __builtin_nontemporal_load(reinterpret_cast<const nvk_u32x4*>(kp));
+      buf.v[i] = __builtin_nontemporal_load(reinterpret_cast<const nvk_u32x4*>(vp));
+    }
+  }
+}
+
+// Online-softmax state of one lane's row group for the G heads.
+template <int G>
+struct SoftmaxState {
+  float m[G], l[G], o[G][8];
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      m[h] = -INFINITY;
+      l[h] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+    }
+  }
+};
 
 template <int HD, int G>
-__global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
-  constexpr int LPR = HD / 8;          // lanes per K/V row
-  constexpr int RPL = 64 / LPR;        // rows per load instruction
-  constexpr int LOADS = kTile / RPL;   // load instructions per tile
-  static_assert(LOADS % 2 == 0, "P.V pairs keys");
-
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int j = lane % LPR;  // 16-byte chunk of the row: d in [8j, 8j+8)
-  const int g = lane / LPR;  // row within a load instruction
-
-  const int ctx = clamp_ctx(a, b);
-  const int nsplit = (ctx + kSplit - 1) / kSplit;
-
-  __shared__ float s_m[kWaves][G];
-  __shared__ float s_l[kWaves][G];
-  __shared__ float s_o[kWaves][G][HD];
-
-  if (ctx == 0) {
-    // padded graph row: defined zero output (model_runner.py:204-211).
-    if (split == 0) {
-      for (int e = tid; e < G * HD; e += 256) {
-        const int h = e / HD, d = e % HD;
-        a.out[(int64_t)b * a.out_stride_tok + (int64_t)(kvh * G + h) * a.out_stride_head + d] = 0;
-      }
+__device__ __forceinline__ void compute_chunk(const DecodeArgs& a, const ChunkBuf<HD, G>& buf,
+                                              int base, int ctx, int tpi, const LaneRole& r,
+                                              SoftmaxState<G>& st) {
+  using CB = ChunkBuf<HD, G>;
+  float s[G][kLoads];
+#pragma unroll
+  for (int i = 0; i < kLoads; ++i) {
+    const bool ok = base + i * tpi + r.tt < ctx;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float acc = nvk_dot2_bf16(buf.q[h][0], buf.k[i].x, 0.f);
+      acc = nvk_dot2_bf16(buf.q[h][1], buf.k[i].y, acc);
+      acc = nvk_dot2_bf16(buf.q[h][2], buf.k[i].z, acc);
+      acc = nvk_dot2_bf16(buf.q[h][3], buf.k[i].w, acc);
+      acc = nvk_group_sum<CB::LPR>(acc);
+      s[h][i] = ok ? acc * a.scale_log2 : -INFINITY;
     }
-    return;
   }
-  if (split >= nsplit) return;
-
-  // ---- query fragment: q[b, kvh*G + h, 8j : 8j+8] as 4 bf16x2 words -------
-  uint32_t qw[G][4];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const uint16_t* qp = a.q + (int64_t)b * a.q_stride_tok + (int64_t)(kvh * G + h) * a.q_stride_head + 8 * j;
-    const nvk_u32x4 v = *reinterpret_cast<const nvk_u32x4*>(qp);
-    qw[h][0] = v.x; qw[h][1] = v.y; qw[h][2] = v.z; qw[h][3] = v.w;
-  }
-
-  const int32_t* bt_row = a.block_tables + (int64_t)b * a.bt_stride;
-  const int64_t row_elems = (int64_t)a.num_kv_heads * HD;
-  const int64_t head_off = (int64_t)kvh * HD + 8 * j;
-  const int tile_base = split * kSplit + wave * kTile;
-  const bool one_page = (a.block_size % kTile) == 0;
-
-  float m_run[G], l_run[G], o_run[G][8];
+    float mt = s[h][0];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    m_run[h] = -INFINITY;
-    l_run[h] = 0.f;
+    for (int i = 1; i < kLoads; ++i) mt = fmaxf(mt, s[h][i]);
+    const float m_new = fmaxf(st.m[h], mt);
+    const float moff = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = nvk_fast_exp2(st.m[h] - moff);
+    st.m[h] = m_new;
+    float psum = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o_run[h][e] = 0.f;
-  }
-
-  if (tile_base < ctx) {
-    // ---- issue all K and V loads of the tile ---------------------------------
-    int64_t tile_row0 = -1;
-    if (one_page) tile_row0 = nvk_paged_row(bt_row, tile_base, a.block_size, a.bs_shift, a.num_blocks);
-    nvk_u32x4 kr[LOADS], vr[LOADS];
-    bool valid[LOADS];
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int pos = tile_base + i * RPL + g;
-      int64_t row;
-      if (one_page) row = tile_row0 < 0 ? -1 : tile_row0 + i * RPL + g;
-      else row = pos < ctx ? nvk_paged_row(bt_row, pos, a.block_size, a.bs_shift, a.num_blocks) : -1;
-      valid[i] = (pos < ctx) && (row >= 0);
-      kr[i] = nvk_u32x4{0, 0, 0, 0};
-      if (valid[i]) kr[i] = *reinterpret_cast<const nvk_u32x4*>(a.k_cache + row * row_elems + head_off);
+    for (int i = 0; i < kLoads; ++i) {
+      s[h][i] = nvk_fast_exp2(s[h][i] - moff);
+      psum += s[h][i];
     }
+    st.l[h] = st.l[h] * alpha + psum;
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
-      const int pos = tile_base + i * RPL + g;
-      int64_t row;
-      if (one_page) row = tile_row0 < 0 ? -1 : tile_row0 + i * RPL + g;
-      else row = pos < ctx ? nvk_paged_row(bt_row, pos, a.block_size, a.bs_shift, a.num_blocks) : -1;
-      vr[i] = nvk_u32x4{0, 0, 0, 0};
-      if (valid[i]) vr[i] = *reinterpret_cast<const nvk_u32x4*>(a.v_cache + row * row_elems + head_off);
-    }
-
-    // ---- scores s[h][i] (already in log2 units) --------------------------------
-    float s[G][LOADS];
+    for (int e = 0; e < 8; ++e) st.o[h][e] *= alpha;
+  }
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) {
+  for (int i = 0; i < kLoads; i += 2) {
+    uint32_t pk[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) pk[h] = nvk_pack_bf16x2(s[h][i], s[h][i + 1]);
+    const uint32_t va[4] = {buf.v[i].x, buf.v[i].y, buf.v[i].z, buf.v[i].w};
+    const uint32_t vb[4] = {buf.v[i + 1].x, buf.v[i + 1].y, buf.v[i + 1].z, buf.v[i + 1].w};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t even = __builtin_amdgcn_perm(vb[w], va[w], 0x05040100u);  // (va.lo, vb.lo)
+      const uint32_t odd = __builtin_amdgcn_perm(vb[w], va[w], 0x07060302u);   // (va.hi, vb.hi)
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        float acc = nvk_dot2_bf16(qw[h][0], kr[i].x, 0.f);
-        acc = nvk_dot2_bf16(qw[h][1], kr[i].y, acc);
-        acc = nvk_dot2_bf16(qw[h][2], kr[i].z, acc);
-        acc = nvk_dot2_bf16(qw[h][3], kr[i].w, acc);
-        acc = group_sum_row<HD>(acc);
-        s[h][i] = valid[i] ? acc * a.scale_log2 : -INFINITY;
+        st.o[h][2 * w] = nvk_dot2_bf16(pk[h], even, st.o[h][2 * w]);
+        st.o[h][2 * w + 1] = nvk_dot2_bf16(pk[h], odd, st.o[h][2 * w + 1]);
       }
     }
+  }
+}
 
-    // ---- online softmax over the tile ------------------------------------------
+// Merges the row groups that hold the same kv head (they differ by multiples
+// of `stride` lanes; `tpi` of them).  Afterwards the lanes with tt == 0 hold
+// the head's state.
+template <int G>
+__device__ __forceinline__ void merge_same_head(SoftmaxState<G>& st, int tpi, int stride) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float mt = s[h][0];
+  for (int h = 0; h < G; ++h) {
+    float M = st.m[h];
+    for (int s = stride; s < stride * tpi; s <<= 1) M = fmaxf(M, xor_lane(M, s));
+    const float w = (M == -INFINITY) ? 0.f : nvk_fast_exp2(st.m[h] - M);
+    float l = st.l[h] * w;
+    for (int s = stride; s < stride * tpi; s <<= 1) l += xor_lane(l, s);
+    st.m[h] = M;
+    st.l[h] = l;
 #pragma unroll
-      for (int i = 1; i < LOADS; ++i) mt = fmaxf(mt, s[h][i]);
-      mt = cross_group_max<HD>(mt);
-      m_run[h] = mt;  // first (and only) tile of this wave
-      const float moff = (mt == -INFINITY) ? 0.f : mt;
-      float lsum = 0.f;
-#pragma unroll
-      for (int i = 0; i < LOADS; ++i) {
-        s[h][i] = nvk_fast_exp2(s[h][i] - moff);
-        lsum += s[h][i];
-      }
-      l_run[h] = lsum;
+    for (int e = 0; e < 8; ++e) {
+      float o = st.o[h][e] * w;
+      for (int s = stride; s < stride * tpi; s <<= 1) o += xor_lane(o, s);
+      st.o[h][e] = o;
     }
+  }
+}
 
-    // ---- P.V with bf16-pair dot products ---------------------------------------
+__device__ __forceinline__ void store_bf16x8(uint16_t* p, const float* v, float scale) {
+  nvk_u32x4 w;
+  w.x = nvk_pack_bf16x2(v[0] * scale, v[1] * scale);
+  w.y = nvk_pack_bf16x2(v[2] * scale, v[3] * scale);
+  w.z = nvk_pack_bf16x2(v[4] * scale, v[5] * scale);
+  w.w = nvk_pack_bf16x2(v[6] * scale, v[7] * scale);
+  *reinterpret_cast<nvk_u32x4*>(p) = w;
+}
+
+template <int HD, int G, bool ALIGNED>
+__global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
+  using CB = ChunkBuf<HD, G>;
+  constexpr int RPI = 64 / CB::LPR;           // head rows per load instruction
+  constexpr int REC_HEAD = G * (HD + 4);      // floats per head in a record
+  __shared__ int s_cs[kMaxBatch + 1];
+  __shared__ int s_wsum[kWavesPerWG];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int hpi = a.hpi;
+  const int tpi = RPI / hpi;
+  LaneRole role;
+  role.j = lane % CB::LPR;
+  const int g = lane / CB::LPR;
+  role.hh = g % hpi;
+  role.tt = g / hpi;
+  const int n_blk = a.num_kv_heads / hpi;
+
+  const int S = chunk_prefix(a, s_cs, s_wsum);
+  if (blockIdx.x == 0) {  // empty contexts: no wave visits them
+    for (int e = tid; e < a.batch * n_blk; e += 256) {
+      const int b = e / n_blk;
+      if (s_cs[b + 1] == s_cs[b]) *reinterpret_cast<int2*>(a.ws_desc + 2 * e) = make_int2(-1, -1);
+    }
+  }
+  const int64_t T = (int64_t)n_blk * S;
+  const int64_t P = active_waves(T, a.n_waves);
+  // the wave index is wave-uniform; say so, so that the range bookkeeping and
+  // the page-table reads stay scalar
+  const int64_t w = (int64_t)blockIdx.x * kWavesPerWG + uniform(tid >> 6);
+  if (w >= P) return;
+  const int64_t c0 = range_begin(w, T, P), c1 = range_begin(w + 1, T, P);
+  if (c0 >= c1) return;
+
+  // locate chunk c0: last b with n_blk*s_cs[b] <= c0
+  int lo = 0, hi = a.batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)n_blk * uniform(s_cs[mid]) <= c0) lo = mid; else hi = mid - 1;
+  }
+  ChunkPos cur;
+  cur.b = uniform(lo);
+  cur.n = uniform(s_cs[cur.b + 1] - s_cs[cur.b]);
+  const int r = (int)(c0 - (int64_t)n_blk * s_cs[cur.b]);
+  cur.blk = uniform(r / cur.n);
+  cur.k = uniform(r % cur.n);
+  bool started_here = cur.k == 0;
+  int ctx = clamp_ctx(a, cur.b);
+
+  SoftmaxState<G> st;
+  st.reset();
+  CB buf;
+  for (int64_t c = c0;; ++c) {
+    load_chunk<HD, G, ALIGNED>(a, cur, ctx, role, tpi, buf);
+    compute_chunk<HD, G>(a, buf, cur.k * a.tc, ctx, tpi, role, st);
+    const bool last = c + 1 == c1;
+    const bool group_end = cur.k == cur.n - 1;
+    if (group_end || last) {
+      if (tpi > 1) merge_same_head<G>(st, tpi, hpi * CB::LPR);
+      const int kvh = cur.blk * hpi + role.hh;
+      const bool whole = group_end && started_here;
+      if (role.tt == 0) {
+        if (whole) {
 #pragma unroll
-    for (int i = 0; i < LOADS; i += 2) {
-      uint32_t pk[G];
+          for (int h = 0; h < G; ++h) {
+            const float inv = st.l[h] > 0.f ? 1.f / st.l[h] : 0.f;
+            store_bf16x8(a.out + (int64_t)cur.b * a.out_stride_tok +
+                             (int64_t)(kvh * G + h) * a.out_stride_head + 8 * role.j,
+                         st.o[h], inv);
+          }
+        } else {
+          float* rec = a.ws_rec + ((w * 2 + (started_here ? 0 : 1)) * hpi + role.hh) * REC_HEAD;
 #pragma unroll
-      for (int h = 0; h < G; ++h) pk[h] = nvk_pack_bf16x2(s[h][i], s[h][i + 1]);
-      const uint32_t va[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
-      const uint32_t vb[4] = {vr[i + 1].x, vr[i + 1].y, vr[i + 1].z, vr[i + 1].w};
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t even = __builtin_amdgcn_perm(vb[w], va[w], 0x05040100u);  // (va.lo, vb.lo)
-        const uint32_t odd = __builtin_amdgcn_perm(vb[w], va[w], 0x07060302u);   // (va.hi, vb.hi)
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          o_run[h][2 * w] = nvk_dot2_bf16(pk[h], even, o_run[h][2 * w]);
-          o_run[h][2 * w + 1] = nvk_dot2_bf16(pk[h], odd, o_run[h][2 * w + 1]);
+          for (int h = 0; h < G; ++h) {
+            float* ro = rec + h * (HD + 4);
+            *reinterpret_cast<nvk_f32x4*>(ro + 8 * role.j) =
+                nvk_f32x4{st.o[h][0], st.o[h][1], st.o[h][2], st.o[h][3]};
+            *reinterpret_cast<nvk_f32x4*>(ro + 8 * role.j + 4) =
+                nvk_f32x4{st.o[h][4], st.o[h][5], st.o[h][6], st.o[h][7]};
+            if (role.j == 0) {
+              ro[HD] = st.m[h];
+              ro[HD + 1] = st.l[h];
+            }
+          }
         }
       }
-    }
-
-    // ---- reduce the row groups of the wave ------------------------------------
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      l_run[h] = cross_group_sum<HD>(l_run[h]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o_run[h][e] = cross_group_sum<HD>(o_run[h][e]);
-    }
-  }
-
-  // ---- merge the 4 waves in LDS -----------------------------------------------
-  if (g == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s_o[wave][h][8 * j + e] = o_run[h][e];
-    }
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      s_m[wave][h] = m_run[h];
-      s_l[wave][h] = l_run[h];
-    }
-  }
-  __syncthreads();
-
-  const int q_head0 = kvh * G;
-  for (int e = tid; e < G * HD; e += 256) {
-    const int h = e / HD, d = e % HD;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][h]);
-    float L = 0.f, O = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float wt = nvk_fast_exp2(s_m[w][h] - M);  // exp2(-inf) = 0 for empty waves
-        L += s_l[w][h] * wt;
-        O += s_o[w][h][d] * wt;
+      if (lane == 0) {  // group descriptor: first and last wave of the group
+        const int64_t gfirst = (int64_t)n_blk * s_cs[cur.b] + (int64_t)cur.blk * cur.n;
+        const int p1 = (int)chunk_owner(gfirst, T, P);
+        const int p2 = (int)chunk_owner(gfirst + cur.n - 1, T, P);
+        *reinterpret_cast<int2*>(a.ws_desc + 2 * (cur.b * n_blk + cur.blk)) = make_int2(p1, p2);
       }
+      st.reset();
+      started_here = true;
     }
-    if (nsplit == 1) {
-      const float r = L > 0.f ? O / L : 0.f;
-      a.out[(int64_t)b * a.out_stride_tok + (int64_t)(q_head0 + h) * a.out_stride_head + d] =
-          __builtin_bit_cast(uint16_t, (__bf16)r);
-    } else {
-      const int64_t part = ((int64_t)b * a.num_q_heads + q_head0 + h) * a.max_splits + split;
-      a.ws_o[part * HD + d] = O;
-      if (d == 0) {
-        a.ws_ml[2 * part] = M;
-        a.ws_ml[2 * part + 1] = L;
-      }
-    }
+    if (last) return;
+    const int b_prev = cur.b;
+    advance(cur, s_cs, n_blk);
+    if (cur.b != b_prev) ctx = clamp_ctx(a, cur.b);
   }
 }
 
-// Combines the split partials of sequences with more than one split.
-// grid = (Hq, B), block = HD threads (one output element each).
-template <int HD>
-__global__ __launch_bounds__(HD) void paged_decode_combine_kernel(DecodeArgs a) {
-  const int h = blockIdx.x;
-  const int b = blockIdx.y;
-  const int d = threadIdx.x;
-  const int ctx = clamp_ctx(a, b);
-  const int nsplit = (ctx + kSplit - 1) / kSplit;
-  if (nsplit <= 1) return;
-  const int64_t part0 = ((int64_t)b * a.num_q_heads + h) * a.max_splits;
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ws_ml[2 * (part0 + s)]);
-  float L = 0.f, O = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < nsplit; ++s) {
-      const float wt = nvk_fast_exp2(a.ws_ml[2 * (part0 + s)] - M);
-      L += a.ws_ml[2 * (part0 + s) + 1] * wt;
-      O += a.ws_o[(part0 + s) * HD + d] * wt;
-    }
+// Merges the partial records of groups cut between waves and writes the zero
+// output of empty contexts.  grid = (Hkv, B), block = G*HD threads.
+template <int HD, int G>
+__global__ __launch_bounds__(G * HD) void paged_decode_combine_kernel(DecodeArgs a) {
+  constexpr int REC_HEAD = G * (HD + 4);
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int h = threadIdx.x / HD, d = threadIdx.x % HD;
+  const int n_blk = a.num_kv_heads / a.hpi;
+  const int hh = kvh % a.hpi;
+  const int2 desc = *reinterpret_cast<const int2*>(a.ws_desc + 2 * (b * n_blk + kvh / a.hpi));
+  uint16_t* op = a.out + (int64_t)b * a.out_stride_tok + (int64_t)(kvh * G + h) * a.out_stride_head + d;
+  if (desc.x < 0) {  // empty context (padded graph row): defined zero output
+    *op = 0;
+    return;
   }
-  const float r = L > 0.f ? O / L : 0.f;
-  a.out[(int64_t)b * a.out_stride_tok + (int64_t)h * a.out_stride_head + d] =
-      __builtin_bit_cast(uint16_t, (__bf16)r);
+  const int p1 = desc.x, p2 = desc.y;
+  if (p1 == p2) return;  // finished inside one wave
+  // Parts: wave p1's head record (slot 0) and the continuation records
+  // (slot 1) of waves p1+1 .. p2 (every active wave's range holds at least
+  // kMinChunks chunks, so each of them wrote one).  kBatch parts are fetched
+  // per round trip (48 loads in flight), then folded into (M, L, O).
+  constexpr int kBatch = 16;
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int base = p1; base <= p2; base += kBatch) {
+    float mv[kBatch], lv[kBatch], ov[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int p = base + u;
+      const bool ok = p <= p2;
+      const int pr = ok ? p : p1;
+      const float* rec = a.ws_rec + (((int64_t)pr * 2 + (pr == p1 ? 0 : 1)) * a.hpi + hh) * REC_HEAD +
+                         h * (HD + 4);
+      mv[u] = rec[HD];
+      lv[u] = rec[HD + 1];
+      ov[u] = rec[d];
+      if (!ok) mv[u] = -INFINITY;
+    }
+    float mb = M;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) mb = fmaxf(mb, mv[u]);
+    if (mb == -INFINITY) continue;
+    const float r = nvk_fast_exp2(M - mb);  // 0 while M is still -inf
+    L *= r;
+    O *= r;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const float wt = nvk_fast_exp2(mv[u] - mb);
+      L += lv[u] * wt;
+      O += ov[u] * wt;
+    }
+    M = mb;
+  }
+  *op = __builtin_bit_cast(uint16_t, (__bf16)(L > 0.f ? O / L : 0.f));
 }
 
-int decode_max_splits(int block_size, int max_blocks) {
-  const int64_t cap = (int64_t)block_size * max_blocks;
-  return (int)((cap + kSplit - 1) / kSplit);
+// kv heads per load instruction.  One: a group is then one (sequence, kv
+// head), so a context is cut into fewer parts and the combine pass reads them
+// in a single round trip.  Measured on MI355X (Qwen3 decode step), reading 4
+// heads per instruction (1 KiB contiguous) streams no faster than 1 head
+// (4 x 256 B), and quadruples the parts per cut group.
+int decode_hpi(int num_kv_heads, int head_dim) {
+  (void)num_kv_heads;
+  (void)head_dim;
+  return 1;
+}
+
+int decode_tc(int num_kv_heads, int head_dim) {
+  const int rpi = 64 / (head_dim / 8);
+  return kLoads * (rpi / decode_hpi(num_kv_heads, head_dim));
+}
+
+// Waves of the persistent grid for these static sizes.
+int decode_waves(int batch, int num_kv_heads, int head_dim, int block_size, int max_blocks) {
+  const int tc = decode_tc(num_kv_heads, head_dim);
+  const int64_t max_chunks_seq = ((int64_t)block_size * max_blocks + tc - 1) / tc;
+  const int64_t t_max = max_chunks_seq * batch * (num_kv_heads / decode_hpi(num_kv_heads, head_dim));
+  int64_t wgs = (t_max / kMinChunks + kWavesPerWG - 1) / kWavesPerWG;
+  if (wgs > kMaxWGs) wgs = kMaxWGs;
+  if (wgs < 1) wgs = 1;
+  return (int)wgs * kWavesPerWG;
+}
+
+size_t decode_ws_bytes(int batch, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                       int max_blocks) {
+  const int G = num_q_heads / num_kv_heads;
+  const size_t P = decode_waves(batch, num_kv_heads, head_dim, block_size, max_blocks);
+  const size_t hpi = decode_hpi(num_kv_heads, head_dim);
+  const size_t desc = ((size_t)batch * (num_kv_heads / hpi) * 8 + 255) / 256 * 256;
+  return desc + P * 2 * hpi * G * (head_dim + 4) * sizeof(float);
 }
 
 template <int HD, int G>
-int launch_decode(const DecodeArgs& a, hipStream_t stream) {
-  dim3 grid(a.max_splits, a.num_kv_heads, a.batch);
-  hipLaunchKernelGGL((paged_decode_kernel<HD, G>), grid, dim3(256), 0, stream, a);
+int launch_decode(const DecodeArgs& a, bool aligned, hipStream_t stream) {
+  const dim3 grid(a.n_waves / kWavesPerWG);
+  if (aligned)
+    hipLaunchKernelGGL((paged_decode_kernel<HD, G, true>), grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((paged_decode_kernel<HD, G, false>), grid, dim3(256), 0, stream, a);
   int st = nvk_launch_status();
   if (st != NVK_OK) return st;
-  if (a.max_splits > 1) {
-    hipLaunchKernelGGL((paged_decode_combine_kernel<HD>), dim3(a.num_q_heads, a.batch), dim3(HD), 0,
-                       stream, a);
-    st = nvk_launch_status();
-  }
-  return st;
+  hipLaunchKernelGGL((paged_decode_combine_kernel<HD, G>), dim3(a.num_kv_heads, a.batch),
+                     dim3(G * HD), 0, stream, a);
+  return nvk_launch_status();
 }
 
 template <int HD>
-int dispatch_group(const DecodeArgs& a, int G, hipStream_t s) {
+int dispatch_group(const DecodeArgs& a, int G, bool aligned, hipStream_t s) {
   switch (G) {
-    case 1: return launch_decode<HD, 1>(a, s);
-    case 2: return launch_decode<HD, 2>(a, s);
-    case 4: return launch_decode<HD, 4>(a, s);
-    case 8: return launch_decode<HD, 8>(a, s);
+    case 1: return launch_decode<HD, 1>(a, aligned, s);
+    case 2: return launch_decode<HD, 2>(a, aligned, s);
+    case 4: return launch_decode<HD, 4>(a, aligned, s);
+    case 8: return launch_decode<HD, 8>(a, aligned, s);
     default: return NVK_EUNSUPPORTED;
   }
 }
@@ -329,14 +553,12 @@ int dispatch_group(const DecodeArgs& a, int G, hipStream_t s) {
 }  // namespace
 
 extern "C" size_t nvk_paged_decode_workspace_size(int32_t batch, int32_t num_q_heads,
-                                                  int32_t head_dim, int32_t block_size,
-                                                  int32_t max_blocks) {
-  if (batch <= 0 || num_q_heads <= 0 || head_dim <= 0 || block_size <= 0 || max_blocks <= 0)
+                                                  int32_t num_kv_heads, int32_t head_dim,
+                                                  int32_t block_size, int32_t max_blocks) {
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 ||
+      max_blocks <= 0 || num_q_heads % num_kv_heads || (head_dim != 64 && head_dim != 128))
     return 0;
-  const int S = decode_max_splits(block_size, max_blocks);
-  if (S <= 1) return 0;
-  const size_t parts = (size_t)batch * num_q_heads * S;
-  return parts * (size_t)head_dim * sizeof(float) + parts * 2 * sizeof(float);
+  return decode_ws_bytes(batch, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks);
 }
 
 extern "C" int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -354,17 +576,27 @@ extern "C" int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_s
   if (dtype != NVK_DTYPE_BF16) return NVK_EUNSUPPORTED;
   if (num_q_heads % num_kv_heads) return NVK_EINVAL;
   if (head_dim != 64 && head_dim != 128) return NVK_EUNSUPPORTED;
+  const int G = num_q_heads / num_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return NVK_EUNSUPPORTED;
   if (batch == 0) return NVK_OK;
+  if (batch > kMaxBatch || num_kv_heads > 65535) return NVK_EUNSUPPORTED;
   if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out) return NVK_EINVAL;
   if (bt_stride < max_blocks) return NVK_EINVAL;
-  // 16-byte vector access of q / K / V rows.
-  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16) return NVK_EALIGN;
-  if ((q_stride_tok % 8) || (q_stride_head % 8) || ((uintptr_t)out % 2)) return NVK_EALIGN;
-  if (batch > 65535) return NVK_EINVAL;
+  if ((int64_t)block_size * max_blocks > INT32_MAX) return NVK_EINVAL;
+  const int tc = decode_tc(num_kv_heads, head_dim);
+  // chunk counts are 32-bit: batch * chunks per sequence * head blocks must fit
+  if ((int64_t)batch * num_kv_heads * (((int64_t)block_size * max_blocks + tc - 1) / tc) >
+      INT32_MAX)
+    return NVK_EINVAL;
+  // 16-byte vector access of q / K / V rows and of the output rows.
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out) % 16)
+    return NVK_EALIGN;
+  if ((q_stride_tok % 8) || (q_stride_head % 8) || (out_stride_tok % 8) || (out_stride_head % 8))
+    return NVK_EALIGN;
   const size_t need =
-      nvk_paged_decode_workspace_size(batch, num_q_heads, head_dim, block_size, max_blocks);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return NVK_EWORKSPACE;
-  if (need > 0 && ((uintptr_t)workspace % 16)) return NVK_EALIGN;
+      decode_ws_bytes(batch, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks);
+  if (workspace == nullptr || workspace_bytes < need) return NVK_EWORKSPACE;
+  if ((uintptr_t)workspace % 256) return NVK_EALIGN;
 
   DecodeArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -386,12 +618,14 @@ extern "C" int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_s
   a.out = static_cast<uint16_t*>(out);
   a.out_stride_tok = out_stride_tok;
   a.out_stride_head = out_stride_head;
-  a.max_splits = decode_max_splits(block_size, max_blocks);
-  const size_t parts = (size_t)batch * num_q_heads * a.max_splits;
-  a.ws_o = need ? static_cast<float*>(workspace) : nullptr;
-  a.ws_ml = need ? static_cast<float*>(workspace) + parts * head_dim : nullptr;
-  const int G = num_q_heads / num_kv_heads;
+  a.hpi = decode_hpi(num_kv_heads, head_dim);
+  a.tc = tc;
+  a.n_waves = decode_waves(batch, num_kv_heads, head_dim, block_size, max_blocks);
+  const size_t desc = ((size_t)batch * (num_kv_heads / a.hpi) * 8 + 255) / 256 * 256;
+  a.ws_desc = static_cast<int32_t*>(workspace);
+  a.ws_rec = reinterpret_cast<float*>(static_cast<char*>(workspace) + desc);
+  const bool aligned = (block_size % tc) == 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (head_dim == 128) return dispatch_group<128>(a, G, s);
-  return dispatch_group<64>(a, G, s);
+  if (head_dim == 128) return dispatch_group<128>(a, G, aligned, s);
+  return dispatch_group<64>(a, G, aligned, s);
 }

@@ -110,7 +110,8 @@ def paged_decode(q, k_cache, v_cache, context_lens, block_table, softmax_scale, 
     scale = float(softmax_scale) if softmax_scale is not None else d ** -0.5
     lib = _lib.load()
     max_blocks = bt.shape[1]
-    ws_bytes = lib.nvk_paged_decode_workspace_size(b, hq, d, block_size, max_blocks)
+    ws_bytes = lib.nvk_paged_decode_workspace_size(b, hq, hkv, d, block_size, max_blocks)
+    # torch's caching allocator hands out 512-byte aligned blocks (graph-pool safe)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     with torch.cuda.device(dev):
         code = lib.nvk_paged_decode(

@@ -59,8 +59,14 @@ def test_error_codes_without_launching():
     # workspace too small
     small_ws = list(args); small_ws[20] = 16
     assert lib.nvk_paged_decode(*small_ws, 0, None) == -4
-    assert lib.nvk_paged_decode_workspace_size(64, 16, 128, 256, 8) == 64 * 16 * 8 * (128 + 2) * 4
-    assert lib.nvk_paged_decode_workspace_size(4, 16, 128, 256, 1) == 0
+    # group descriptors (8 bytes per (sequence, kv head), 256-byte padded) + 2
+    # records per wave of the persistent grid, each holding 1 kv head x 2 q
+    # heads; B=64, 8 kv heads, 2048-token tables: 512 workgroups x 4 waves
+    assert lib.nvk_paged_decode_workspace_size(64, 16, 8, 128, 256, 8) == \
+        4096 + 2048 * 2 * 1 * 2 * (128 + 4) * 4
+    # tiny problem: one wave per chunk (B=1, 1 kv head, 64-token table: 2 chunks -> 1 WG)
+    assert lib.nvk_paged_decode_workspace_size(1, 2, 1, 128, 64, 1) == 256 + 4 * 2 * 2 * 132 * 4
+    assert lib.nvk_paged_decode_workspace_size(4, 16, 5, 128, 256, 1) == 0   # 16 % 5 != 0
     # prefill: head_dim 64 not built
     assert lib.nvk_varlen_prefill(16, 2048, 128, 4, 16, 16, 1024, 1024, 128, 4, 16, 16, 1, 4, None,
                                   0, 0, 0, 0, 16, 8, 64, 0.1, 16, 2048, 128, 0, None) == -2
