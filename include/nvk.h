@@ -104,8 +104,9 @@ int nvk_kv_store(const void* key, int64_t key_row_stride,
  *   or stale, model_runner.py:123-127, 204-211).
  * context_lens: int32 [batch]; it counts the token just stored
  *   (model_runner.py:180).  context_lens[b] == 0 (a padded graph row) writes
- *   zeros.  Lengths above max_blocks*block_size are clamped to it; page ids
- *   outside [0, num_blocks) contribute no keys.
+ *   zeros.  Lengths above max_blocks*block_size are clamped to it.  A page id
+ *   outside [0, num_blocks) is never dereferenced; the output of a context
+ *   that names one is unspecified (the reference reads out of bounds there).
  * workspace: device scratch of nvk_paged_decode_workspace_size() bytes, 256-byte
  *   aligned (per-context descriptors and the partial results of contexts split
  *   between waves); it need not be initialised, every call writes what it
@@ -148,7 +149,8 @@ size_t nvk_paged_decode_workspace_size(int32_t batch, int32_t num_q_heads,
  *   [num_blocks][block_size][num_kv_heads][head_dim] (contiguous; k_stride_tok,
  *   v_stride_tok and kv_stride_head are ignored) and key j of sequence s lives
  *   in page block_tables[s*bt_stride + j/block_size].  Lk is clamped to
- *   max_blocks*block_size; page ids outside [0, num_blocks) contribute no keys.
+ *   max_blocks*block_size.  A page id outside [0, num_blocks) is never
+ *   dereferenced; the output of a sequence that names one is unspecified.
  * Dense mode (block_tables == NULL): k / v are [total_k][num_kv_heads][head_dim]
  *   with row strides k_stride_tok / v_stride_tok and head stride kv_stride_head;
  *   key j of sequence s is row cu_seqlens_k[s] + j (rows >= total_k are

@@ -58,20 +58,22 @@ struct PrefillArgs {
   int n_qtiles;
 };
 
-// Element offset of (key position pos, kv head) in k (is_v=false) or v, or -1.
-__device__ __forceinline__ int64_t kv_offset(const PrefillArgs& a, const int32_t* bt_row,
-                                             int64_t k_row0, int pos, int kvh, bool is_v) {
-  if (a.block_tables) {
-    const int64_t row = nvk_paged_row(bt_row, pos, a.block_size, a.bs_shift, a.num_blocks);
-    if (row < 0) return -1;
-    return row * ((int64_t)a.num_kv_heads * HD) + (int64_t)kvh * HD;
-  }
-  const int64_t row = k_row0 + pos;
-  if (row >= a.total_k) return -1;
-  return row * (is_v ? a.v_stride_tok : a.k_stride_tok) + (int64_t)kvh * a.kv_stride_head;
+// How a workgroup finds its keys.
+enum KvMode {
+  kDense = 0,         // k / v rows of the step, key j of sequence s = row cu_k[s] + j
+  kPagedAligned = 1,  // paged, block_size a multiple of 64: a key tile lies in one page
+  kPagedAny = 2,      // paged, any other block size
+};
+
+// Raw buffer resource over [base, base + bytes): a load at an offset >= bytes
+// returns zeros and touches no memory.  dword3 0x00020000 = 32-bit data
+// format, the gfx9 setting for untyped buffer loads.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint16_t* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, (int)bytes,
+                                           0x00020000);
 }
 
-template <int G>
+template <int G, int MODE>
 __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   constexpr int TQ = kRows / G;  // query tokens per workgroup
 
@@ -92,9 +94,12 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   if (Lq <= 0 || q0 + TQ <= 0) return;
 
   int Lk_eff = Lk;
-  if (a.block_tables) {
+  if (MODE != kDense) {
     const int64_t cap = (int64_t)a.max_blocks * a.block_size;
     if ((int64_t)Lk_eff > cap) Lk_eff = (int)cap;
+  } else {
+    const int64_t cap = a.total_k - k_row0;  // rows past the end of k / v are absent
+    if ((int64_t)Lk_eff > cap) Lk_eff = cap > 0 ? (int)cap : 0;
   }
   const int diag = Lk - Lq;                    // row i sees keys j <= i + diag
   int n_keys = (q0 + TQ - 1) + diag + 1;       // keys visible to the last row
@@ -105,7 +110,7 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sK[kKeys * kKPad];
   __shared__ __attribute__((aligned(16))) uint16_t sVt[HD * kVPad];
 
-  const int32_t* bt_row = a.block_tables ? a.block_tables + (int64_t)s * a.bt_stride : nullptr;
+  const int32_t* bt_row = MODE != kDense ? a.block_tables + (int64_t)s * a.bt_stride : nullptr;
 
   // ---- this lane's query row and its Q fragment (B operand of S^T) --------
   const int row = wave * 32 + l32;
@@ -136,25 +141,79 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   const int v_kg_perm = (v_kg & ~3) | ((v_kg & 1) << 1) | ((v_kg & 2) >> 1);
 
   nvk_u32x4 kst[4], vst[4];
+  // Dense and aligned-paged tiles: the tile's keys are consecutive rows of one
+  // buffer, so each tile gets one buffer resource sized to its valid rows; a
+  // key past the end (or on an invalid page) falls outside it and loads zeros.
+  // The page id of the next tile is fetched one tile ahead, so no load waits
+  // on the block table.
+  const uint32_t k_row_bytes =
+      MODE == kDense ? (uint32_t)a.k_stride_tok * 2u : (uint32_t)a.num_kv_heads * HD * 2u;
+  const uint32_t v_row_bytes =
+      MODE == kDense ? (uint32_t)a.v_stride_tok * 2u : (uint32_t)a.num_kv_heads * HD * 2u;
+  const int last_page = n_keys > 0 ? (n_keys - 1) / a.block_size : 0;
+  auto fetch_page = [&](int kt) -> int {
+    int logical = a.bs_shift >= 0 ? (kt * kKeys) >> a.bs_shift : (kt * kKeys) / a.block_size;
+    logical = logical < last_page ? logical : last_page;
+    asm volatile("" : "+v"(logical));  // keep the table read a vector load
+    return bt_row[logical];
+  };
+  int page_next = 0;
+  if (MODE == kPagedAligned && n_keys > 0) page_next = fetch_page(0);
+
+  // kPagedAny: per-key page lookup; a missing key reads the sequence's first q
+  // row (finite), its score is masked to -inf and its probability is 0.
+  const uint16_t* dummy = a.q + (int64_t)q_row0 * a.q_stride_tok;
+  const int64_t paged_row_elems = (int64_t)a.num_kv_heads * HD;
+
   auto load_tile = [&](int kt) {
     const int base = kt * kKeys;
+    if constexpr (MODE == kPagedAny) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int pos = base + k_key0 + 16 * i;
-      kst[i] = nvk_u32x4{0, 0, 0, 0};
-      if (pos < n_keys) {
-        const int64_t off = kv_offset(a, bt_row, k_row0, pos, kvh, false);
-        if (off >= 0) kst[i] = *reinterpret_cast<const nvk_u32x4*>(a.k + off + 8 * k_dc);
+      for (int i = 0; i < 4; ++i) {
+        const int pos = base + k_key0 + 16 * i;
+        const int64_t r = pos < n_keys ? nvk_paged_row(bt_row, pos, a.block_size, a.bs_shift,
+                                                       a.num_blocks) : -1;
+        const uint16_t* p = r >= 0 ? a.k + r * paged_row_elems + kvh * HD + 8 * k_dc : dummy;
+        kst[i] = *reinterpret_cast<const nvk_u32x4*>(p);
       }
-    }
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int pos = base + 4 * v_kg + jj;
-      vst[jj] = nvk_u32x4{0, 0, 0, 0};
-      if (pos < n_keys) {
-        const int64_t off = kv_offset(a, bt_row, k_row0, pos, kvh, true);
-        if (off >= 0) vst[jj] = *reinterpret_cast<const nvk_u32x4*>(a.v + off + 8 * v_dc);
+      for (int jj = 0; jj < 4; ++jj) {
+        const int pos = base + 4 * v_kg + jj;
+        const int64_t r = pos < n_keys ? nvk_paged_row(bt_row, pos, a.block_size, a.bs_shift,
+                                                       a.num_blocks) : -1;
+        const uint16_t* p = r >= 0 ? a.v + r * paged_row_elems + kvh * HD + 8 * v_dc : dummy;
+        vst[jj] = *reinterpret_cast<const nvk_u32x4*>(p);
       }
+    } else {
+      const int rem = n_keys - base < kKeys ? n_keys - base : kKeys;  // valid rows, > 0
+      const uint16_t* kb;
+      const uint16_t* vb;
+      uint32_t k_bytes = (uint32_t)rem * k_row_bytes;
+      uint32_t v_bytes = (uint32_t)rem * v_row_bytes;
+      if constexpr (MODE == kDense) {
+        kb = a.k + (int64_t)(k_row0 + base) * a.k_stride_tok + (int64_t)kvh * a.kv_stride_head;
+        vb = a.v + (int64_t)(k_row0 + base) * a.v_stride_tok + (int64_t)kvh * a.kv_stride_head;
+      } else {
+        const int page = __builtin_amdgcn_readfirstlane(page_next);
+        if (kt + 1 < (n_keys + kKeys - 1) / kKeys) page_next = fetch_page(kt + 1);
+        const int logical = a.bs_shift >= 0 ? base >> a.bs_shift : base / a.block_size;
+        const int64_t row = (int64_t)page * a.block_size + (base - logical * a.block_size);
+        const bool ok = (uint32_t)page < (uint32_t)a.num_blocks;
+        kb = ok ? a.k + row * paged_row_elems + kvh * HD : a.k;
+        vb = ok ? a.v + row * paged_row_elems + kvh * HD : a.v;
+        k_bytes = ok ? k_bytes : 0u;
+        v_bytes = ok ? v_bytes : 0u;
+      }
+      const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kb, k_bytes);
+      const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vb, v_bytes);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        kst[i] = __builtin_bit_cast(nvk_u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+            rk, (k_key0 + 16 * i) * k_row_bytes + 16 * k_dc, 0, 0));
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        vst[jj] = __builtin_bit_cast(nvk_u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+            rv, (4 * v_kg + jj) * v_row_bytes + 16 * v_dc, 0, 0));
     }
   };
   auto store_tile = [&]() {
@@ -283,7 +342,12 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
 template <int G>
 int launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   dim3 grid(a.num_kv_heads, a.batch, a.n_qtiles);
-  hipLaunchKernelGGL((varlen_prefill_kernel<G>), grid, dim3(256), 0, stream, a);
+  if (!a.block_tables)
+    hipLaunchKernelGGL((varlen_prefill_kernel<G, kDense>), grid, dim3(256), 0, stream, a);
+  else if (a.block_size % kKeys == 0)
+    hipLaunchKernelGGL((varlen_prefill_kernel<G, kPagedAligned>), grid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((varlen_prefill_kernel<G, kPagedAny>), grid, dim3(256), 0, stream, a);
   return nvk_launch_status();
 }
 
@@ -314,8 +378,13 @@ extern "C" int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q
   if (block_tables) {
     if (block_size <= 0 || max_blocks <= 0 || num_blocks < 0 || bt_stride < max_blocks)
       return NVK_EINVAL;
+    // a key tile's byte offsets are 32-bit: 64 rows of num_kv_heads*head_dim
+    if ((int64_t)num_kv_heads * HD >= (1 << 23)) return NVK_EINVAL;
   } else {
     if (k_stride_tok % 8 || v_stride_tok % 8 || kv_stride_head % 8) return NVK_EALIGN;
+    if (k_stride_tok < HD || v_stride_tok < HD || k_stride_tok >= (1 << 23) ||
+        v_stride_tok >= (1 << 23) || kv_stride_head < 0)
+      return NVK_EINVAL;
   }
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16) return NVK_EALIGN;
   if ((q_stride_tok % 8) || (q_stride_head % 8)) return NVK_EALIGN;
