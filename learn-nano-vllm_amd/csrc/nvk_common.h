@@ -15,6 +15,8 @@ typedef float nvk_f32x4 __attribute__((ext_vector_type(4)));
 typedef float nvk_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t nvk_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t nvk_u32x2 __attribute__((ext_vector_type(2)));
+typedef short nvk_i16x4 __attribute__((ext_vector_type(4)));
+typedef short nvk_i16x8 __attribute__((ext_vector_type(8)));
 
 // log2(e): softmax is evaluated as exp2(x*log2e - m), v_exp_f32 being base 2.
 #define NVK_LOG2E 1.4426950408889634f
@@ -71,6 +73,28 @@ template <int MASK>
 NVK_DEVICE float nvk_xor_lane(float x) {
   const int lane = __lane_id();
   return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ MASK) << 2, __float_as_int(x)));
+}
+
+// max(a, b, c) as one v_max3_f32.  fmaxf would first quiet each operand
+// (v_max x, x) since the MFMA results it reads are not known to be canonical;
+// the scores here are never NaN unless the inputs are.
+NVK_DEVICE float nvk_max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// max / sum of x over lanes l and l ^ 32, with v_permlane32_swap (a VALU
+// exchange of the two wave halves, no LDS round trip).
+NVK_DEVICE float nvk_max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+NVK_DEVICE float nvk_sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 NVK_DEVICE float nvk_fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

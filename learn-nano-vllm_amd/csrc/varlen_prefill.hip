@@ -13,31 +13,37 @@
 //   * A workgroup = 4 waves owns one (sequence, kv head, query tile).  The
 //     tile has 128 rows = (128/G) query tokens x the G query heads that share
 //     the kv head, so every K/V tile staged in LDS feeds all G heads.  Row r
-//     is token r/G, head r%G.
-//   * Per 64-key tile: K is staged row-major in LDS ([key][d], padded), V is
-//     staged transposed ([d][key], padded) with keys permuted inside each
-//     group of 16 (bits 2 and 3 swapped).
-//   * S^T = K Q^T uses v_mfma_f32_32x32x16_bf16 with K (from LDS) as the A
-//     operand and the wave's Q fragment (registers, loaded once) as B.  In the
-//     32x32 accumulator each lane then holds 32 keys of ONE query row, so the
-//     row max / sum of the online softmax need one cross-lane step (lane^32).
-//   * O^T = V^T P^T uses the same MFMA with V^T (from LDS) as A and the
-//     probabilities as B straight from the S^T accumulators: the key order in
-//     which a lane holds its 8 probabilities per 16-key step is exactly the
-//     permuted order of the V^T tile, so P never leaves the registers.
-//   * Global loads of the next key tile are issued before the MFMAs of the
-//     current one (register staging); the grid runs the query tiles nearest
-//     the end of each sequence (the ones with most keys) first.
+//     is token r/G, head r%G; wave w owns rows 32w..32w+31.
+//   * K and V tiles of 64 keys go from HBM straight into LDS (buffer/global
+//     loads with the LDS destination, 16 bytes per lane), row-major [key][d]
+//     with 256-byte rows whose 16-byte chunks are XOR-swizzled by the row, so
+//     both MFMA operand reads below are bank-conflict free.
+//   * S^T = K Q^T: v_mfma_f32_32x32x16_bf16 with K (LDS) as the A operand and
+//     the wave's Q fragment (registers, loaded once) as B.  Each lane then
+//     holds 32 keys of ONE query row; the row max / sum need one exchange of
+//     the wave halves (v_permlane32_swap).
+//   * O^T += V^T P^T: the same MFMA with V^T as A, read with the transposing
+//     LDS load (ds_read_b64_tr_b16), and P as B straight from the S^T
+//     accumulators (P never leaves the registers).
+//   * Software pipeline, one barrier per key tile: while tile t is in its
+//     softmax (VALU) and PV product, the S MFMAs of tile t+1 run and the loads
+//     of K(t+2) and V(t+1) are in flight into the free LDS stages.
+//   * Softmax in log2 units with a lazily updated reference max (rescaling
+//     only when a tile raises the max by more than 2^8), row sums by
+//     v_dot2_f32_bf16 over the packed probabilities.
+//   * The grid runs the query tiles nearest the end of each sequence (the
+//     ones with most keys) first.
 #include "nvk_common.h"
 
 namespace {
 
 constexpr int HD = 128;
 constexpr int kWaves = 4;
-constexpr int kRows = 128;       // query rows per workgroup
-constexpr int kKeys = 64;        // keys per tile
-constexpr int kKPad = HD + 8;    // sK row stride (elements)
-constexpr int kVPad = kKeys + 8; // sVt row stride (elements)
+constexpr int kRows = 128;                   // query rows per workgroup
+constexpr int kKeys = 64;                    // keys per tile
+constexpr int kRowBytes = HD * 2;            // LDS bytes of one key row
+constexpr int kTileBytes = kKeys * kRowBytes;
+constexpr float kLazy = 8.f;                 // log2 headroom of the lazy softmax max
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -65,12 +71,47 @@ enum KvMode {
   kPagedAny = 2,      // paged, any other block size
 };
 
-// Raw buffer resource over [base, base + bytes): a load at an offset >= bytes
-// returns zeros and touches no memory.  dword3 0x00020000 = 32-bit data
-// format, the gfx9 setting for untyped buffer loads.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint16_t* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, (int)bytes,
-                                           0x00020000);
+// Raw buffer descriptor over [base, base + bytes) (stride 0, dword3 0x00020000
+// = 32-bit data format, the gfx9 setting for untyped buffer access).
+__device__ __forceinline__ nvk_u32x4 tile_rsrc(const uint16_t* base, uint32_t bytes) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  return nvk_u32x4{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, bytes, 0x00020000u};
+}
+
+// 16-byte chunk c of key row r sits at chunk c ^ swz(r) of the LDS row.  Over
+// any 16 consecutive rows swz is a bijection (the K operand reads one chunk of
+// 16 rows per 16 lanes) and over 4 consecutive rows it spreads 4 chunks over
+// 16 slots (the transposing V reads).
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)(lds_ptr_t)(p);
+}
+
+// Loads straight into LDS, 16 bytes per lane: lane l of the wave writes LDS
+// bytes [dst + 16 l, dst + 16 l + 16).  Issued as inline asm so that the
+// compiler does not order the wave's later LDS reads (of other stages) behind
+// them; completion is awaited explicitly (vmcnt) before the publishing barrier.
+// `rsrc`: a raw buffer descriptor (wave-uniform); loads at offsets >= its
+// size write zeros.
+// The descriptor and the LDS address are wave-uniform; readfirstlane puts
+// them in SGPRs where the compiler computed them with vector instructions.
+__device__ __forceinline__ void lds_load_buffer(const nvk_u32x4& rsrc, uint32_t voffset,
+                                                uint32_t dst) {
+  auto u = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); };
+  const nvk_u32x4 r = {u(rsrc.x), u(rsrc.y), u(rsrc.z), u(rsrc.w)};
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :: "v"(voffset), "s"(r), "s"((uint32_t)__builtin_amdgcn_readfirstlane((int)dst))
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_load_global(const void* src, uint32_t dst) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"((uint32_t)__builtin_amdgcn_readfirstlane((int)dst)) : "memory", "m0");
+}
+__device__ __forceinline__ void wait_lds_loads() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 template <int G, int MODE>
@@ -81,7 +122,7 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   const int s = blockIdx.y;
   const int qt = blockIdx.z;  // 0 = the tile that ends at the last query token
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int half = lane >> 5;  // 0/1: which 8-wide k slice this lane feeds
   const int l32 = lane & 31;
@@ -104,11 +145,15 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   const int diag = Lk - Lq;                    // row i sees keys j <= i + diag
   int n_keys = (q0 + TQ - 1) + diag + 1;       // keys visible to the last row
   if (n_keys > Lk_eff) n_keys = Lk_eff;
+  if (n_keys < 0) n_keys = 0;
   const int t_first = q0 < 0 ? 0 : q0;
-  const int unmasked_keys = t_first + diag + 1;  // keys visible to every valid row
+  const int unmasked_keys = t_first + diag + 1;  // keys visible to every row of the tile
+  const int n_tiles = (n_keys + kKeys - 1) / kKeys;
 
-  __shared__ __attribute__((aligned(16))) uint16_t sK[kKeys * kKPad];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[HD * kVPad];
+  // LDS: K stages 0/1, then V stages 0/1 (64 KB).
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kTileBytes];
+  auto k_stage = [&](int st) { return lds + st * kTileBytes; };
+  auto v_stage = [&](int st) { return lds + (2 + st) * kTileBytes; };
 
   const int32_t* bt_row = MODE != kDense ? a.block_tables + (int64_t)s * a.bt_stride : nullptr;
 
@@ -131,25 +176,82 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   }
   const int row_limit = tok + diag;  // last visible key of this row
 
-  // ---- loader roles ----------------------------------------------------------
-  // K: chunk c = tid + 256*i -> key (tid>>4) + 16 i, d chunk (tid & 15).
-  // V: keys 4*(tid&15) .. +3, d chunk (tid >> 4).
-  const int k_key0 = tid >> 4;
-  const int k_dc = tid & 15;
-  const int v_kg = tid & 15;
-  const int v_dc = tid >> 4;
-  const int v_kg_perm = (v_kg & ~3) | ((v_kg & 1) << 1) | ((v_kg & 2) >> 1);
-
-  nvk_u32x4 kst[4], vst[4];
-  // Dense and aligned-paged tiles: the tile's keys are consecutive rows of one
-  // buffer, so each tile gets one buffer resource sized to its valid rows; a
-  // key past the end (or on an invalid page) falls outside it and loads zeros.
-  // The page id of the next tile is fetched one tile ahead, so no load waits
-  // on the block table.
+  // ---- tile loads straight into LDS ---------------------------------------------
+  // Wave w fills rows 16w..16w+15 of a stage with 4 loads of 4 rows; lane l
+  // writes LDS chunk l of the load, i.e. row 16w + 4j + l/16, slot l%16, so
+  // it fetches chunk (l%16) ^ swz(row) of that key row.
+  const int dma_rsub = lane >> 4;  // row within the 4-row block
+  auto dma_chunk = [&](int j) { return (lane & 15) ^ ((dma_rsub << 2) | j); };
   const uint32_t k_row_bytes =
       MODE == kDense ? (uint32_t)a.k_stride_tok * 2u : (uint32_t)a.num_kv_heads * HD * 2u;
   const uint32_t v_row_bytes =
       MODE == kDense ? (uint32_t)a.v_stride_tok * 2u : (uint32_t)a.num_kv_heads * HD * 2u;
+  const int64_t paged_row_elems = (int64_t)a.num_kv_heads * HD;
+  // kPagedAny: a key that does not exist reads the sequence's first q row
+  // (finite); its score is masked to -inf and its probability is 0.
+  const uint16_t* dummy = a.q + (int64_t)q_row0 * a.q_stride_tok;
+
+  // A K or V tile load into one LDS stage, planned once per tile and issued as
+  // 4 instructions (load j fills rows 16w+4j .. +3 of the wave's quarter), so
+  // the issues can be spread over the MFMA work.  Dense / aligned paged: one
+  // buffer descriptor per load over the valid rows only (rows past them load
+  // zeros); a tile that does not exist has 0 valid rows.  kPagedAny: per-row
+  // global addresses, resolved when the plan is made.
+  struct DmaPlan {
+    const uint16_t* tb;    // row 0 of the tile (head kvh)
+    int bytes;             // valid bytes from tb (rows * row_bytes)
+    uint32_t row_bytes;
+    uint32_t dst0;         // LDS byte address of the wave's first row
+    const uint16_t* rows[4];  // kPagedAny: this lane's source per load
+  };
+  auto plan_tile = [&](int kt, uint8_t* dst, bool is_v, int page) {
+    DmaPlan pl;
+    const int base = kt * kKeys;
+    const uint16_t* src = is_v ? a.v : a.k;
+    pl.dst0 = lds_addr(dst + 16 * wave * kRowBytes);
+    pl.row_bytes = is_v ? v_row_bytes : k_row_bytes;
+    int rem = n_keys - base < kKeys ? n_keys - base : kKeys;
+    rem = rem > 0 ? rem : 0;
+    if constexpr (MODE == kPagedAny) {
+      pl.tb = src;
+      pl.bytes = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int pos = base + 16 * wave + 4 * j + dma_rsub;
+        const int64_t prow = pos < n_keys ? nvk_paged_row(bt_row, pos, a.block_size, a.bs_shift,
+                                                          a.num_blocks) : -1;
+        pl.rows[j] = (prow >= 0 ? src + prow * paged_row_elems + kvh * HD : dummy) +
+                     8 * dma_chunk(j);
+      }
+    } else {
+      pl.bytes = rem * (int)pl.row_bytes;
+      if constexpr (MODE == kDense) {
+        pl.tb = src + (int64_t)(k_row0 + base) * (is_v ? a.v_stride_tok : a.k_stride_tok) +
+                (int64_t)kvh * a.kv_stride_head;
+      } else {
+        const int logical = a.bs_shift >= 0 ? base >> a.bs_shift : base / a.block_size;
+        const int64_t prow = (int64_t)page * a.block_size + (base - logical * a.block_size);
+        const bool ok = (uint32_t)page < (uint32_t)a.num_blocks && rem > 0;
+        pl.tb = ok ? src + prow * paged_row_elems + kvh * HD : src;
+        pl.bytes = ok ? pl.bytes : 0;
+      }
+    }
+    return pl;
+  };
+  auto issue_load = [&](const DmaPlan& pl, int j) {
+    if constexpr (MODE == kPagedAny) {
+      lds_load_global(pl.rows[j], pl.dst0 + 4 * j * kRowBytes);
+    } else {
+      const int skip = (16 * wave + 4 * j) * (int)pl.row_bytes;
+      int left = pl.bytes - skip;
+      left = left > 0 ? left : 0;
+      const uint32_t voff = (uint32_t)dma_rsub * pl.row_bytes +
+                            16u * (uint32_t)((lane & 15) ^ ((dma_rsub << 2) | j));
+      lds_load_buffer(tile_rsrc(pl.tb + skip / 2, (uint32_t)left), voff, pl.dst0 + 4 * j * kRowBytes);
+    }
+  };
+
+  // Page ids (kPagedAligned): read one step before the tile's load is issued.
   const int last_page = n_keys > 0 ? (n_keys - 1) / a.block_size : 0;
   auto fetch_page = [&](int kt) -> int {
     int logical = a.bs_shift >= 0 ? (kt * kKeys) >> a.bs_shift : (kt * kKeys) / a.block_size;
@@ -157,173 +259,257 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
     asm volatile("" : "+v"(logical));  // keep the table read a vector load
     return bt_row[logical];
   };
-  int page_next = 0;
-  if (MODE == kPagedAligned && n_keys > 0) page_next = fetch_page(0);
 
-  // kPagedAny: per-key page lookup; a missing key reads the sequence's first q
-  // row (finite), its score is masked to -inf and its probability is 0.
-  const uint16_t* dummy = a.q + (int64_t)q_row0 * a.q_stride_tok;
-  const int64_t paged_row_elems = (int64_t)a.num_kv_heads * HD;
-
-  auto load_tile = [&](int kt) {
-    const int base = kt * kKeys;
-    if constexpr (MODE == kPagedAny) {
+  // ---- S^T = K Q^T for one tile: two 32-key blocks ---------------------------
+  // Lane reads key row 32 mb + l32, logical chunk 2 ks + half, i.e. byte
+  // row*256 + 16*((2 ks + half) ^ swz(row)) = k_addr ^ (32 ks) (+ 8192 mb).
+  const int k_swz = swz(l32);
+  const uint32_t k_addr0 = lds_addr(lds) + l32 * kRowBytes + 16 * ((half ^ k_swz) & 1) +
+                           32 * (k_swz >> 1);
+  auto compute_s = [&](int stage, nvk_f32x16 (&acc)[2]) {
+    uint32_t ka = k_addr0 + stage * kTileBytes;
+    asm volatile("" : "+v"(ka));  // rebuilt every tile: keeps 8 addresses out of registers
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int pos = base + k_key0 + 16 * i;
-        const int64_t r = pos < n_keys ? nvk_paged_row(bt_row, pos, a.block_size, a.bs_shift,
-                                                       a.num_blocks) : -1;
-        const uint16_t* p = r >= 0 ? a.k + r * paged_row_elems + kvh * HD + 8 * k_dc : dummy;
-        kst[i] = *reinterpret_cast<const nvk_u32x4*>(p);
+    for (int mb = 0; mb < 2; ++mb) acc[mb] = nvk_f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) {
+      const uint32_t addr = ka ^ (32u * ks);
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const nvk_bf16x8 kf = *reinterpret_cast<const __attribute__((address_space(3)))
+                                                    nvk_bf16x8*>((size_t)(addr + 32 * kRowBytes * mb));
+        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], acc[mb], 0, 0, 0);
       }
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int pos = base + 4 * v_kg + jj;
-        const int64_t r = pos < n_keys ? nvk_paged_row(bt_row, pos, a.block_size, a.bs_shift,
-                                                       a.num_blocks) : -1;
-        const uint16_t* p = r >= 0 ? a.v + r * paged_row_elems + kvh * HD + 8 * v_dc : dummy;
-        vst[jj] = *reinterpret_cast<const nvk_u32x4*>(p);
-      }
-    } else {
-      const int rem = n_keys - base < kKeys ? n_keys - base : kKeys;  // valid rows, > 0
-      const uint16_t* kb;
-      const uint16_t* vb;
-      uint32_t k_bytes = (uint32_t)rem * k_row_bytes;
-      uint32_t v_bytes = (uint32_t)rem * v_row_bytes;
-      if constexpr (MODE == kDense) {
-        kb = a.k + (int64_t)(k_row0 + base) * a.k_stride_tok + (int64_t)kvh * a.kv_stride_head;
-        vb = a.v + (int64_t)(k_row0 + base) * a.v_stride_tok + (int64_t)kvh * a.kv_stride_head;
-      } else {
-        const int page = __builtin_amdgcn_readfirstlane(page_next);
-        if (kt + 1 < (n_keys + kKeys - 1) / kKeys) page_next = fetch_page(kt + 1);
-        const int logical = a.bs_shift >= 0 ? base >> a.bs_shift : base / a.block_size;
-        const int64_t row = (int64_t)page * a.block_size + (base - logical * a.block_size);
-        const bool ok = (uint32_t)page < (uint32_t)a.num_blocks;
-        kb = ok ? a.k + row * paged_row_elems + kvh * HD : a.k;
-        vb = ok ? a.v + row * paged_row_elems + kvh * HD : a.v;
-        k_bytes = ok ? k_bytes : 0u;
-        v_bytes = ok ? v_bytes : 0u;
-      }
-      const __amdgpu_buffer_rsrc_t rk = tile_rsrc(kb, k_bytes);
-      const __amdgpu_buffer_rsrc_t rv = tile_rsrc(vb, v_bytes);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        kst[i] = __builtin_bit_cast(nvk_u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-            rk, (k_key0 + 16 * i) * k_row_bytes + 16 * k_dc, 0, 0));
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        vst[jj] = __builtin_bit_cast(nvk_u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-            rv, (4 * v_kg + jj) * v_row_bytes + 16 * v_dc, 0, 0));
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<nvk_u32x4*>(&sK[(k_key0 + 16 * i) * kKPad + 8 * k_dc]) = kst[i];
-    const uint32_t r0[4] = {vst[0].x, vst[0].y, vst[0].z, vst[0].w};
-    const uint32_t r1[4] = {vst[1].x, vst[1].y, vst[1].z, vst[1].w};
-    const uint32_t r2[4] = {vst[2].x, vst[2].y, vst[2].z, vst[2].w};
-    const uint32_t r3[4] = {vst[3].x, vst[3].y, vst[3].z, vst[3].w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-      nvk_u32x2 w;
-      w.x = __builtin_amdgcn_perm(r1[e >> 1], r0[e >> 1], sel);
-      w.y = __builtin_amdgcn_perm(r3[e >> 1], r2[e >> 1], sel);
-      *reinterpret_cast<nvk_u32x2*>(&sVt[(8 * v_dc + e) * kVPad + 4 * v_kg_perm]) = w;
     }
   };
 
+  // ---- O^T += V^T P^T -----------------------------------------------------------
+  // A operand lane l: V^T[d = 32 db + l%32][8 keys], from two ds_read_b64_tr_b16:
+  // inside a 16-lane group, source lane c names the 4 elements at key kb + c/4,
+  // d d0 + 4(c%4), and lane i receives V[kb + 0..3][d0 + i].  The fragment's
+  // keys are {4h..4h+3, 8+4h..8+4h+3} (h = lane/32) of the 16-key step: the
+  // order in which the S^T accumulator holds P.  Byte address of the lo/hi read
+  // for d block db: v_lo/hi ^ (64 db) (+ 4096 ks).
   nvk_f32x16 acc_o[HD / 32];
 #pragma unroll
   for (int db = 0; db < HD / 32; ++db) acc_o[db] = nvk_f32x16{};
-  float m_run = -INFINITY;  // running max, log2 units (already scaled)
-  float l_run = 0.f;        // this lane's share of the row sum
+  uint32_t v_lo0, v_hi0;
+  {
+    const int tr_key = (lane & 15) >> 2;                          // row within the 4-row group
+    const int tr_c0 = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);  // chunk within 32 d
+    const int sw_lo = swz(4 * half + tr_key), sw_hi = swz(8 + 4 * half + tr_key);
+    const uint32_t v0 = lds_addr(lds) + 2 * kTileBytes + 8 * (lane & 1);
+    v_lo0 = v0 + (4 * half + tr_key) * kRowBytes + 16 * (tr_c0 ^ (sw_lo & 3)) + 64 * (sw_lo >> 2);
+    v_hi0 = v0 + (8 + 4 * half + tr_key) * kRowBytes + 16 * (tr_c0 ^ (sw_hi & 3)) +
+            64 * (sw_hi >> 2);
+  }
+  // Online softmax in log2 units with a lazily updated reference max: the
+  // probabilities are exp2(score - m_ref) with m_ref at most kLazy below the
+  // true running max, so they stay <= 2^kLazy; m_ref (and the accumulators)
+  // are only rescaled when a tile's max exceeds m_ref + kLazy.
+  float m_ref = -INFINITY;
+  float l_part[2] = {0.f, 0.f};  // this lane's share of the row sum (two chains)
 
-  const int n_tiles = n_keys > 0 ? (n_keys + kKeys - 1) / kKeys : 0;
-  if (n_tiles > 0) load_tile(0);
-
-  for (int kt = 0; kt < n_tiles; ++kt) {
-    store_tile();
-    __syncthreads();
-    if (kt + 1 < n_tiles) load_tile(kt + 1);
-
-    // ---- S^T = K Q^T : two 32-key blocks ------------------------------------
-    nvk_f32x16 acc_s[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      acc_s[mb] = nvk_f32x16{};
-      const uint16_t* kp = &sK[(32 * mb + l32) * kKPad + 8 * half];
-#pragma unroll
-      for (int ks = 0; ks < HD / 16; ++ks) {
-        const nvk_bf16x8 kf = *reinterpret_cast<const nvk_bf16x8*>(kp + 16 * ks);
-        acc_s[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], acc_s[mb], 0, 0, 0);
-      }
-    }
-
-    // ---- mask (only tiles that cross the diagonal or the end of the keys) ---
+  // Masks the tile (boundary tiles only), takes its row max and rescales when
+  // the max moved past the headroom; returns the offset for exp2.
+  auto softmax_max = [&](nvk_f32x16 (&sc)[2], int kt) -> float {
     const int kbase = kt * kKeys;
-    if (kbase + kKeys > unmasked_keys || kbase + kKeys > n_keys || !row_valid) {
+    if (kbase + kKeys > unmasked_keys || kbase + kKeys > n_keys) {  // uniform
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = kbase + 32 * mb + 8 * (i >> 2) + 4 * half + (i & 3);
-          const bool vis = row_valid && key <= row_limit && key < n_keys;
-          acc_s[mb][i] = vis ? acc_s[mb][i] : -INFINITY;
+          sc[mb][i] = (key <= row_limit && key < n_keys) ? sc[mb][i] : -INFINITY;
         }
       }
     }
-
-    // ---- online softmax (row = l32, keys split across lane halves) ----------
-    float mt = -INFINITY;
+    float mx = nvk_max3(sc[0][0], sc[0][1], sc[0][2]);
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int i = 3; i < 15; i += 2) mx = nvk_max3(mx, sc[0][i], sc[0][i + 1]);
+    mx = nvk_max3(mx, sc[0][15], sc[1][0]);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mt = fmaxf(mt, acc_s[mb][i]);
+    for (int i = 1; i < 15; i += 2) mx = nvk_max3(mx, sc[1][i], sc[1][i + 1]);
+    mx = fmaxf(mx, sc[1][15]);
+    const float mt = nvk_max_xor32(mx) * a.scale_log2;
+    const bool need = mt > m_ref + kLazy;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      const float m_new = need ? mt : m_ref;
+      const float alpha = nvk_fast_exp2(m_ref - m_new);  // 0 when m_ref = -inf
+      m_ref = m_new;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) l_part[j] *= alpha;
+#pragma unroll
+      for (int db = 0; db < HD / 32; ++db) acc_o[db] *= alpha;
     }
-    mt = fmaxf(mt, nvk_xor_lane<32>(mt)) * a.scale_log2;
-    const float m_new = fmaxf(m_run, mt);
-    const float moff = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = nvk_fast_exp2(m_run - moff);
-    m_run = m_new;
-    float psum = 0.f;
+    return m_ref == -INFINITY ? 0.f : m_ref;  // row masked so far: p = 0
+  };
+  // Word e of P fragment p (keys 16p..16p+15 of the tile, in accumulator
+  // order): exp2(score * scale_log2 - moff) of two scores packed to bf16; the
+  // row sum accumulates the same rounded values that enter the PV product.
+  auto exp_word = [&](const nvk_f32x16 (&sc)[2], float moff, int p, int e) -> uint32_t {
+    constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1, 1)
+    const int mb = p >> 1, i = 8 * (p & 1) + 2 * e;
+    const float p0 = nvk_fast_exp2(fmaf(sc[mb][i], a.scale_log2, -moff));
+    const float p1 = nvk_fast_exp2(fmaf(sc[mb][i + 1], a.scale_log2, -moff));
+    const uint32_t w = nvk_pack_bf16x2(p0, p1);
+    l_part[e & 1] = nvk_dot2_bf16(w, kOnes, l_part[e & 1]);
+    return w;
+  };
+
+  // The MFMA work of step kt, software-pipelined by hand (sched_barrier(0)
+  // fences keep the order; the compiler would otherwise group the MFMAs).
+  // P fragment f holds keys 16f..16f+15 of tile kt; fragments 0-1 come from
+  // score block 0, fragments 2-3 from block 1.  Order:
+  //   exp2 of fragment 0;  O k-step 0 (4 MFMAs) with the exp2 of fragment 1;
+  //   S(kt+1) block 0 (8 MFMAs, into the consumed score block 0) with the
+  //   exp2 of fragments 2-3;  S(kt+1) block 1 (8);  O k-steps 1-3 (12).
+  // Ending on O MFMAs lets the next step's row max find S(kt+1) complete.
+  // The loads of V(kt+1) and K(kt+2) are issued between the MFMAs; LDS
+  // operands are read two MFMAs ahead.
+  auto mma_step = [&](int kt, nvk_f32x16 (&sc)[2], float moff, const DmaPlan& plan_v,
+                      const DmaPlan& plan_k) {
+    uint32_t ka = k_addr0 + ((kt + 1) & 1) * kTileBytes;
+    uint32_t va_lo = v_lo0 + (kt & 1) * kTileBytes, va_hi = v_hi0 + (kt & 1) * kTileBytes;
+    asm volatile("" : "+v"(ka), "+v"(va_lo), "+v"(va_hi));  // rebuilt per step
+    auto rd_k = [&](int ks, int mb) {
+      return *reinterpret_cast<const __attribute__((address_space(3))) nvk_bf16x8*>(
+          (size_t)((ka ^ (32u * ks)) + 32 * kRowBytes * mb));
+    };
+    auto rd_v = [&](int db, int ks) {
+      const nvk_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) nvk_i16x4*)(size_t)((va_lo ^ (64u * db)) +
+                                                                  16 * ks * kRowBytes));
+      const nvk_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) nvk_i16x4*)(size_t)((va_hi ^ (64u * db)) +
+                                                                  16 * ks * kRowBytes));
+      const nvk_i16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      return __builtin_bit_cast(nvk_bf16x8, w);
+    };
+    auto pack = [](const uint32_t (&w)[4]) {
+      return __builtin_bit_cast(nvk_bf16x8, nvk_u32x4{w[0], w[1], w[2], w[3]});
+    };
     nvk_bf16x8 pf[4];
+    uint32_t pw[4], pw3[4];
+    nvk_bf16x8 vf[3];
+    vf[0] = rd_v(0, 0);
+    vf[1] = rd_v(1, 0);
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int e = 0; e < 4; ++e) pw[e] = exp_word(sc, moff, 0, e);
+    pf[0] = pack(pw);
+    __builtin_amdgcn_sched_barrier(0);
+    // O k-step 0 with fragment 1.
+    constexpr int kO = (kKeys / 16) * (HD / 32);
+    auto o_mfma = [&](int idx) {  // idx = ks*4 + db; reads V two MFMAs ahead
+      const int ks = idx / (HD / 32), db = idx % (HD / 32);
+      if (idx + 2 < kO) vf[(idx + 2) % 3] = rd_v((idx + 2) % (HD / 32), (idx + 2) / (HD / 32));
+      __builtin_amdgcn_sched_barrier(0);
+      acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[idx % 3], pf[ks], acc_o[db], 0, 0, 0);
+    };
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        uint32_t w[4];
+    for (int idx = 0; idx < 4; ++idx) {
+      o_mfma(idx);
+      pw[idx] = exp_word(sc, moff, 1, idx);
+      if (idx == 1) issue_load(plan_v, 0);
+      if (idx == 3) issue_load(plan_v, 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    pf[1] = pack(pw);
+    // S(kt+1): block 0 with fragments 2-3, then block 1.  After the last tile
+    // this multiplies a stale (or zero-filled) K stage; the result is unused.
+    {
+      nvk_bf16x8 kf[3];
+      kf[0] = rd_k(0, 0);
+      kf[1] = rd_k(1, 0);
+      sc[0] = nvk_f32x16{};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = nvk_fast_exp2(fmaf(acc_s[mb][8 * sub + 2 * e], a.scale_log2, -moff));
-          const float p1 = nvk_fast_exp2(fmaf(acc_s[mb][8 * sub + 2 * e + 1], a.scale_log2, -moff));
-          psum += p0 + p1;
-          w[e] = nvk_pack_bf16x2(p0, p1);
-        }
-        pf[2 * mb + sub] = __builtin_bit_cast(nvk_bf16x8, nvk_u32x4{w[0], w[1], w[2], w[3]});
+      for (int ks = 0; ks < HD / 16; ++ks) {
+        if (ks + 2 < HD / 16) kf[(ks + 2) % 3] = rd_k(ks + 2, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % 3], qf[ks], sc[0], 0, 0, 0);
+        if (ks < 4) pw[ks] = exp_word(sc, moff, 2, ks);
+        else pw3[ks - 4] = exp_word(sc, moff, 3, ks - 4);
+        if (ks == 2) issue_load(plan_k, 0);
+        if (ks == 6) issue_load(plan_k, 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      pf[2] = pack(pw);
+      pf[3] = pack(pw3);
+      kf[0] = rd_k(0, 1);
+      kf[1] = rd_k(1, 1);
+      sc[1] = nvk_f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < HD / 16; ++ks) {
+        if (ks + 2 < HD / 16) kf[(ks + 2) % 3] = rd_k(ks + 2, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % 3], qf[ks], sc[1], 0, 0, 0);
+        if (ks == 2) issue_load(plan_k, 2);
+        if (ks == 6) issue_load(plan_k, 3);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    l_run = l_run * alpha + psum;
+    // O k-steps 1-3.
 #pragma unroll
-    for (int db = 0; db < HD / 32; ++db) acc_o[db] *= alpha;
+    for (int idx = 4; idx < kO; ++idx) {
+      o_mfma(idx);
+      if (idx == 5) issue_load(plan_v, 2);
+      if (idx == 9) issue_load(plan_v, 3);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
 
-    // ---- O^T += V^T P^T ------------------------------------------------------
+  // ---- pipelined main loop ------------------------------------------------------
+  // Step kt (one barrier): S(kt) is in registers, V(kt) and K(kt+1) are in
+  // LDS.  The step loads V(kt+1) into V stage (kt+1)&1 and K(kt+2) into K
+  // stage kt&1 while it computes O += V(kt) P(kt) and S(kt+1).  The barrier at
+  // the top of a step publishes the previous step's loads (each wave waits for
+  // its own first) and guarantees that every wave has finished reading the
+  // stages this step's loads overwrite.
+  int page_k = 0;      // kPagedAligned: page of tile kt+2 (read one step early)
+  int page_prev = 0;   // page of tile kt+1
+  if (n_tiles > 0) {
+    nvk_f32x16 sc[2];
+    int p0 = 0, p1 = 0;
+    if constexpr (MODE == kPagedAligned) {
+      p0 = __builtin_amdgcn_readfirstlane(fetch_page(0));
+      p1 = n_tiles > 1 ? __builtin_amdgcn_readfirstlane(fetch_page(1)) : 0;
+      if (n_tiles > 2) page_k = fetch_page(2);
+      page_prev = p1;
+    }
+    {
+      const DmaPlan k0 = plan_tile(0, k_stage(0), false, p0);
+      const DmaPlan v0 = plan_tile(0, v_stage(0), true, p0);
+      const DmaPlan k1 = plan_tile(1, k_stage(1), false, p1);
 #pragma unroll
-    for (int db = 0; db < HD / 32; ++db) {
-      const uint16_t* vp = &sVt[(32 * db + l32) * kVPad + 8 * half];
-#pragma unroll
-      for (int ks = 0; ks < kKeys / 16; ++ks) {
-        const nvk_bf16x8 vf = *reinterpret_cast<const nvk_bf16x8*>(vp + 16 * ks);
-        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[ks], acc_o[db], 0, 0, 0);
+      for (int j = 0; j < 4; ++j) {
+        issue_load(k0, j);
+        issue_load(v0, j);
+        issue_load(k1, j);
       }
     }
+    wait_lds_loads();
     __syncthreads();
+    compute_s(0, sc);
+    for (int kt = 0; kt < n_tiles; ++kt) {
+      wait_lds_loads();
+      __syncthreads();
+      int pk = 0, pv = 0;
+      if constexpr (MODE == kPagedAligned) {
+        pk = __builtin_amdgcn_readfirstlane(page_k);
+        pv = page_prev;
+        page_prev = pk;
+        if (kt + 3 < n_tiles) page_k = fetch_page(kt + 3);
+      }
+      const DmaPlan plan_v = plan_tile(kt + 1, v_stage((kt + 1) & 1), true, pv);
+      const DmaPlan plan_k = plan_tile(kt + 2, k_stage(kt & 1), false, pk);
+      const float moff = softmax_max(sc, kt);
+      mma_step(kt, sc, moff, plan_v, plan_k);
+    }
   }
 
   // ---- epilogue: normalise and store the row -----------------------------------
   if (!row_valid) return;
-  const float l_tot = l_run + nvk_xor_lane<32>(l_run);
+  const float l_tot = nvk_sum_xor32(l_part[0] + l_part[1]);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   uint16_t* op = a.out + ((int64_t)q_row0 + tok) * a.out_stride_tok + (int64_t)head * a.out_stride_head;
 #pragma unroll
