@@ -155,7 +155,17 @@ size_t nvk_paged_decode_workspace_size(int32_t batch, int32_t num_q_heads,
  *   with row strides k_stride_tok / v_stride_tok and head stride kv_stride_head;
  *   key j of sequence s is row cu_seqlens_k[s] + j (rows >= total_k are
  *   treated as absent).
- * max_seqlen_q sizes the grid (host value, as in the reference's Context).
+ * max_seqlen_q sizes the grid and max_seqlen_k (0 = unknown) bounds the keys
+ *   of a sequence; both are host values, as in the reference's Context
+ *   (context.py:8-11).  max_seqlen_k only steers the split-K plan: every key
+ *   is still attended if a sequence has more.
+ * workspace: optional device scratch (256-byte aligned) of
+ *   nvk_varlen_prefill_workspace_size() bytes.  When the query tiles alone
+ *   cannot fill the GPU (few, short query ranges over long contexts, e.g.
+ *   speculative-decode verification) the key range is split across
+ *   workgroups whose partial results go to the workspace, and a second kernel
+ *   merges them.  NULL (or too small) = no split; the result is the same up
+ *   to rounding.  Two calls in flight at once need two workspaces.
  * scale must be > 0.  dtype: NVK_DTYPE_BF16.  head_dim: 128.  G: 1, 2, 4 or 8.
  */
 int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -164,13 +174,21 @@ int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_hea
                        int64_t k_stride_tok, int64_t v_stride_tok,
                        int64_t kv_stride_head, int64_t total_k,
                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                       int32_t batch, int32_t max_seqlen_q,
+                       int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k,
                        const int32_t* block_tables, int64_t bt_stride,
                        int32_t max_blocks, int32_t block_size, int32_t num_blocks,
                        int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                        float scale,
                        void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                       void* workspace, size_t workspace_bytes,
                        int32_t dtype, void* stream);
+
+/* Bytes of workspace nvk_varlen_prefill uses to split these sizes (0 = it
+ * does not split them, or bad input).  max_seqlen_k: as in nvk_varlen_prefill
+ * (for a paged call, at most max_blocks*block_size). */
+size_t nvk_varlen_prefill_workspace_size(int32_t batch, int32_t max_seqlen_q,
+                                         int32_t max_seqlen_k, int32_t num_q_heads,
+                                         int32_t num_kv_heads, int32_t head_dim);
 
 #ifdef __cplusplus
 }

@@ -45,6 +45,13 @@ constexpr int kRowBytes = HD * 2;            // LDS bytes of one key row
 constexpr int kTileBytes = kKeys * kRowBytes;
 constexpr float kLazy = 8.f;                 // log2 headroom of the lazy softmax max
 
+// How a workgroup finds its keys.
+enum KvMode {
+  kDense = 0,         // k / v rows of the step, key j of sequence s = row cu_k[s] + j
+  kPagedAligned = 1,  // paged, block_size a multiple of 64: a key tile lies in one page
+  kPagedAny = 2,      // paged, any other block size
+};
+
 struct PrefillArgs {
   const uint16_t* q;
   int64_t q_stride_tok, q_stride_head, total_q;
@@ -62,14 +69,52 @@ struct PrefillArgs {
   uint16_t* out;
   int64_t out_stride_tok, out_stride_head;
   int n_qtiles;
+  // Split-K over key tiles (short query ranges over long contexts): blockIdx.z
+  // = qtile * n_splits + split, split j owning key tiles
+  // [j*tiles_per_split, (j+1)*tiles_per_split) (the last one: to the end).
+  // With n_splits > 1 every row's partial (O unnormalised, m, l) goes to `ws`
+  // and prefill_combine_kernel writes `out`.
+  int n_splits, tiles_per_split;
+  float* ws;
 };
 
-// How a workgroup finds its keys.
-enum KvMode {
-  kDense = 0,         // k / v rows of the step, key j of sequence s = row cu_k[s] + j
-  kPagedAligned = 1,  // paged, block_size a multiple of 64: a key tile lies in one page
-  kPagedAny = 2,      // paged, any other block size
+constexpr int kRecFloats = HD + 4;  // partial record of one row: O[HD], m, l, pad
+
+// Key range of one (sequence, query tile): shared by the attention and the
+// combine kernels.
+struct QTile {
+  int q_row0, Lq, k_row0, Lk;
+  int q0;            // first query token of the tile (may be < 0)
+  int diag;          // row i sees keys j <= i + diag
+  int n_keys;        // keys visible to the last row of the tile (clamped)
+  int unmasked_keys; // keys visible to every row of the tile
+  bool live;         // the tile holds at least one query token
 };
+
+template <int MODE>
+__device__ __forceinline__ QTile qtile_info(const PrefillArgs& a, int s, int qt, int TQ) {
+  QTile t;
+  t.q_row0 = a.cu_q[s];
+  t.Lq = a.cu_q[s + 1] - t.q_row0;
+  t.k_row0 = a.cu_k[s];
+  t.Lk = a.cu_k[s + 1] - t.k_row0;
+  t.q0 = t.Lq - (qt + 1) * TQ;
+  t.live = t.Lq > 0 && t.q0 + TQ > 0;
+  int Lk_eff = t.Lk;
+  if (MODE != kDense) {
+    const int64_t cap = (int64_t)a.max_blocks * a.block_size;
+    if ((int64_t)Lk_eff > cap) Lk_eff = (int)cap;
+  } else {
+    const int64_t cap = a.total_k - t.k_row0;  // rows past the end of k / v are absent
+    if ((int64_t)Lk_eff > cap) Lk_eff = cap > 0 ? (int)cap : 0;
+  }
+  t.diag = t.Lk - t.Lq;
+  int n_keys = (t.q0 + TQ - 1) + t.diag + 1;
+  if (n_keys > Lk_eff) n_keys = Lk_eff;
+  t.n_keys = n_keys < 0 ? 0 : n_keys;
+  t.unmasked_keys = (t.q0 < 0 ? 0 : t.q0) + t.diag + 1;
+  return t;
+}
 
 // Raw buffer descriptor over [base, base + bytes) (stride 0, dword3 0x00020000
 // = 32-bit data format, the gfx9 setting for untyped buffer access).
@@ -120,35 +165,26 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
 
   const int kvh = blockIdx.x;
   const int s = blockIdx.y;
-  const int qt = blockIdx.z;  // 0 = the tile that ends at the last query token
+  const int qt = blockIdx.z / a.n_splits;  // 0 = the tile that ends at the last query token
+  const int split = blockIdx.z - qt * a.n_splits;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int half = lane >> 5;  // 0/1: which 8-wide k slice this lane feeds
   const int l32 = lane & 31;
 
-  const int q_row0 = a.cu_q[s];
-  const int Lq = a.cu_q[s + 1] - q_row0;
-  const int k_row0 = a.cu_k[s];
-  const int Lk = a.cu_k[s + 1] - k_row0;
-  const int q0 = Lq - (qt + 1) * TQ;  // first token of the tile (may be < 0)
-  if (Lq <= 0 || q0 + TQ <= 0) return;
-
-  int Lk_eff = Lk;
-  if (MODE != kDense) {
-    const int64_t cap = (int64_t)a.max_blocks * a.block_size;
-    if ((int64_t)Lk_eff > cap) Lk_eff = (int)cap;
-  } else {
-    const int64_t cap = a.total_k - k_row0;  // rows past the end of k / v are absent
-    if ((int64_t)Lk_eff > cap) Lk_eff = cap > 0 ? (int)cap : 0;
-  }
-  const int diag = Lk - Lq;                    // row i sees keys j <= i + diag
-  int n_keys = (q0 + TQ - 1) + diag + 1;       // keys visible to the last row
-  if (n_keys > Lk_eff) n_keys = Lk_eff;
-  if (n_keys < 0) n_keys = 0;
-  const int t_first = q0 < 0 ? 0 : q0;
-  const int unmasked_keys = t_first + diag + 1;  // keys visible to every row of the tile
+  const QTile qi = qtile_info<MODE>(a, s, qt, TQ);
+  if (!qi.live) return;
+  const int q_row0 = qi.q_row0, Lq = qi.Lq, k_row0 = qi.k_row0;
+  const int q0 = qi.q0, diag = qi.diag, n_keys = qi.n_keys;
+  const int unmasked_keys = qi.unmasked_keys;
   const int n_tiles = (n_keys + kKeys - 1) / kKeys;
+  // This workgroup's key tiles [t_begin, t_end).
+  const int t_begin = split * a.tiles_per_split;
+  const int t_end = split == a.n_splits - 1 ? n_tiles
+                    : (t_begin + a.tiles_per_split < n_tiles ? t_begin + a.tiles_per_split
+                                                             : n_tiles);
+  if (a.n_splits > 1 && t_begin >= t_end) return;  // the combine skips empty splits
 
   // LDS: K stages 0/1, then V stages 0/1 (64 KB).
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kTileBytes];
@@ -211,7 +247,7 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
     pl.dst0 = lds_addr(dst + 16 * wave * kRowBytes);
     pl.row_bytes = is_v ? v_row_bytes : k_row_bytes;
     int rem = n_keys - base < kKeys ? n_keys - base : kKeys;
-    rem = rem > 0 ? rem : 0;
+    rem = (rem > 0 && kt < t_end) ? rem : 0;
     if constexpr (MODE == kPagedAny) {
       pl.tb = src;
       pl.bytes = 0;
@@ -467,19 +503,20 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   // stages this step's loads overwrite.
   int page_k = 0;      // kPagedAligned: page of tile kt+2 (read one step early)
   int page_prev = 0;   // page of tile kt+1
-  if (n_tiles > 0) {
+  if (t_begin < t_end) {
     nvk_f32x16 sc[2];
+    const int tb = t_begin;
     int p0 = 0, p1 = 0;
     if constexpr (MODE == kPagedAligned) {
-      p0 = __builtin_amdgcn_readfirstlane(fetch_page(0));
-      p1 = n_tiles > 1 ? __builtin_amdgcn_readfirstlane(fetch_page(1)) : 0;
-      if (n_tiles > 2) page_k = fetch_page(2);
+      p0 = __builtin_amdgcn_readfirstlane(fetch_page(tb));
+      p1 = tb + 1 < t_end ? __builtin_amdgcn_readfirstlane(fetch_page(tb + 1)) : 0;
+      if (tb + 2 < t_end) page_k = fetch_page(tb + 2);
       page_prev = p1;
     }
     {
-      const DmaPlan k0 = plan_tile(0, k_stage(0), false, p0);
-      const DmaPlan v0 = plan_tile(0, v_stage(0), true, p0);
-      const DmaPlan k1 = plan_tile(1, k_stage(1), false, p1);
+      const DmaPlan k0 = plan_tile(tb, k_stage(tb & 1), false, p0);
+      const DmaPlan v0 = plan_tile(tb, v_stage(tb & 1), true, p0);
+      const DmaPlan k1 = plan_tile(tb + 1, k_stage((tb + 1) & 1), false, p1);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         issue_load(k0, j);
@@ -489,8 +526,8 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
     }
     wait_lds_loads();
     __syncthreads();
-    compute_s(0, sc);
-    for (int kt = 0; kt < n_tiles; ++kt) {
+    compute_s(tb & 1, sc);
+    for (int kt = tb; kt < t_end; ++kt) {
       wait_lds_loads();
       __syncthreads();
       int pk = 0, pv = 0;
@@ -498,7 +535,7 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
         pk = __builtin_amdgcn_readfirstlane(page_k);
         pv = page_prev;
         page_prev = pk;
-        if (kt + 3 < n_tiles) page_k = fetch_page(kt + 3);
+        if (kt + 3 < t_end) page_k = fetch_page(kt + 3);
       }
       const DmaPlan plan_v = plan_tile(kt + 1, v_stage((kt + 1) & 1), true, pv);
       const DmaPlan plan_k = plan_tile(kt + 2, k_stage(kt & 1), false, pk);
@@ -510,6 +547,25 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   // ---- epilogue: normalise and store the row -----------------------------------
   if (!row_valid) return;
   const float l_tot = nvk_sum_xor32(l_part[0] + l_part[1]);
+  if (a.n_splits > 1) {  // partial record: O^T column (unnormalised), m_ref, l
+    float* rec = a.ws + ((((int64_t)s * a.num_kv_heads + kvh) * a.n_qtiles + qt) * a.n_splits +
+                         split) * (int64_t)kRows * kRecFloats +
+                 (int64_t)row * kRecFloats;
+#pragma unroll
+    for (int db = 0; db < HD / 32; ++db) {
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) {
+        const nvk_f32x4 o4 = {acc_o[db][4 * grp], acc_o[db][4 * grp + 1], acc_o[db][4 * grp + 2],
+                              acc_o[db][4 * grp + 3]};
+        *reinterpret_cast<nvk_f32x4*>(rec + 32 * db + 8 * grp + 4 * half) = o4;
+      }
+    }
+    if (half == 0) {
+      rec[HD] = m_ref;
+      rec[HD + 1] = l_tot;
+    }
+    return;
+  }
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   uint16_t* op = a.out + ((int64_t)q_row0 + tok) * a.out_stride_tok + (int64_t)head * a.out_stride_head;
 #pragma unroll
@@ -525,33 +581,138 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   }
 }
 
-template <int G>
-int launch_prefill(const PrefillArgs& a, hipStream_t stream) {
-  dim3 grid(a.num_kv_heads, a.batch, a.n_qtiles);
-  if (!a.block_tables)
-    hipLaunchKernelGGL((varlen_prefill_kernel<G, kDense>), grid, dim3(256), 0, stream, a);
-  else if (a.block_size % kKeys == 0)
-    hipLaunchKernelGGL((varlen_prefill_kernel<G, kPagedAligned>), grid, dim3(256), 0, stream, a);
-  else
-    hipLaunchKernelGGL((varlen_prefill_kernel<G, kPagedAny>), grid, dim3(256), 0, stream, a);
+// Merges the split-K partial records of one (sequence, kv head, query tile):
+// thread t handles row t/2 and d range 64*(t%2) .. +63.
+template <int G, int MODE>
+__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
+  constexpr int TQ = kRows / G;
+  const int kvh = blockIdx.x, s = blockIdx.y, qt = blockIdx.z;
+  const QTile qi = qtile_info<MODE>(a, s, qt, TQ);
+  if (!qi.live) return;
+  const int r = threadIdx.x >> 1, dh = threadIdx.x & 1;
+  const int tok = qi.q0 + r / G;
+  if (tok < 0 || tok >= qi.Lq) return;
+  const int head = kvh * G + r % G;
+  const int n_tiles = (qi.n_keys + kKeys - 1) / kKeys;
+  // splits that own at least one tile (the others wrote nothing)
+  int n_live = a.tiles_per_split > 0 ? (n_tiles + a.tiles_per_split - 1) / a.tiles_per_split : 0;
+  if (n_live > a.n_splits) n_live = a.n_splits;
+  const float* rec0 = a.ws + (((int64_t)s * a.num_kv_heads + kvh) * a.n_qtiles + qt) *
+                                 a.n_splits * (int64_t)kRows * kRecFloats +
+                      (int64_t)r * kRecFloats;
+  const int64_t split_stride = (int64_t)kRows * kRecFloats;
+  float M = -INFINITY;
+  for (int j = 0; j < n_live; ++j) M = fmaxf(M, rec0[j * split_stride + HD]);
+  float L = 0.f;
+  nvk_f32x4 acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = nvk_f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < n_live; ++j) {
+    const float* rec = rec0 + j * split_stride;
+    const float m = rec[HD];
+    const float w = m == -INFINITY ? 0.f : nvk_fast_exp2(m - M);
+    L += w * rec[HD + 1];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const nvk_f32x4 o = *reinterpret_cast<const nvk_f32x4*>(rec + 64 * dh + 4 * i);
+      acc[i] += w * o;
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  uint16_t* op = a.out + ((int64_t)qi.q_row0 + tok) * a.out_stride_tok +
+                 (int64_t)head * a.out_stride_head + 64 * dh;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {  // 8-byte stores: out is only required 8-byte aligned
+    nvk_u32x2 w;
+    w.x = nvk_pack_bf16x2(acc[i][0] * inv, acc[i][1] * inv);
+    w.y = nvk_pack_bf16x2(acc[i][2] * inv, acc[i][3] * inv);
+    *reinterpret_cast<nvk_u32x2*>(op + 4 * i) = w;
+  }
+}
+
+template <int G, int MODE>
+int launch_mode(const PrefillArgs& a, hipStream_t stream) {
+  dim3 grid(a.num_kv_heads, a.batch, a.n_qtiles * a.n_splits);
+  hipLaunchKernelGGL((varlen_prefill_kernel<G, MODE>), grid, dim3(256), 0, stream, a);
+  if (a.n_splits > 1) {
+    const int st = nvk_launch_status();
+    if (st != NVK_OK) return st;
+    dim3 cgrid(a.num_kv_heads, a.batch, a.n_qtiles);
+    hipLaunchKernelGGL((prefill_combine_kernel<G, MODE>), cgrid, dim3(256), 0, stream, a);
+  }
   return nvk_launch_status();
 }
 
+template <int G>
+int launch_prefill(const PrefillArgs& a, hipStream_t stream) {
+  if (!a.block_tables) return launch_mode<G, kDense>(a, stream);
+  if (a.block_size % kKeys == 0) return launch_mode<G, kPagedAligned>(a, stream);
+  return launch_mode<G, kPagedAny>(a, stream);
+}
+
+
+// Split-K plan for a launch: split the key range when the query tiles alone
+// give fewer than ~4 workgroups per CU, keeping at least 8 key tiles (512
+// keys) per split.  Deterministic in its arguments, so the workspace query
+// and the launch agree.
+struct SplitPlan {
+  int n_qtiles, n_splits, tiles_per_split;
+};
+static SplitPlan plan_splits(int batch, int max_seqlen_q, int64_t max_keys, int num_q_heads,
+                             int num_kv_heads) {
+  SplitPlan p;
+  const int G = num_q_heads / num_kv_heads;
+  const int TQ = kRows / G;
+  p.n_qtiles = (max_seqlen_q + TQ - 1) / TQ;
+  p.n_splits = 1;
+  const int64_t max_tiles = (max_keys + kKeys - 1) / kKeys;
+  const int64_t wgs = (int64_t)num_kv_heads * batch * p.n_qtiles;
+  constexpr int64_t kTargetWgs = 1024, kMinTilesPerSplit = 8, kMaxSplits = 16;
+  if (wgs > 0 && wgs < kTargetWgs && max_tiles >= 2 * kMinTilesPerSplit) {
+    int64_t n = (kTargetWgs + wgs - 1) / wgs;
+    if (n > max_tiles / kMinTilesPerSplit) n = max_tiles / kMinTilesPerSplit;
+    if (n > kMaxSplits) n = kMaxSplits;
+    if (p.n_qtiles * n > 65535) n = 1;
+    p.n_splits = n < 1 ? 1 : (int)n;
+  }
+  p.tiles_per_split = (int)((max_tiles + p.n_splits - 1) / p.n_splits);
+  return p;
+}
+static size_t split_workspace_bytes(const SplitPlan& p, int batch, int num_kv_heads) {
+  if (p.n_splits <= 1) return 0;
+  return (size_t)num_kv_heads * batch * p.n_qtiles * p.n_splits * kRows * kRecFloats *
+         sizeof(float);
+}
+
 }  // namespace
+
+extern "C" size_t nvk_varlen_prefill_workspace_size(int32_t batch, int32_t max_seqlen_q,
+                                                    int32_t max_seqlen_k, int32_t num_q_heads,
+                                                    int32_t num_kv_heads, int32_t head_dim) {
+  if (batch <= 0 || max_seqlen_q <= 0 || max_seqlen_k <= 0 || num_q_heads <= 0 ||
+      num_kv_heads <= 0 || head_dim != HD || num_q_heads % num_kv_heads)
+    return 0;
+  const int G = num_q_heads / num_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return 0;
+  return split_workspace_bytes(plan_splits(batch, max_seqlen_q, max_seqlen_k, num_q_heads,
+                                           num_kv_heads),
+                               batch, num_kv_heads);
+}
 
 extern "C" int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                                   int64_t total_q, const void* k, const void* v,
                                   int64_t k_stride_tok, int64_t v_stride_tok,
                                   int64_t kv_stride_head, int64_t total_k,
                                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                                  int32_t batch, int32_t max_seqlen_q,
+                                  int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k,
                                   const int32_t* block_tables, int64_t bt_stride,
                                   int32_t max_blocks, int32_t block_size, int32_t num_blocks,
                                   int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                                   float scale, void* out, int64_t out_stride_tok,
-                                  int64_t out_stride_head, int32_t dtype, void* stream) {
-  if (batch < 0 || max_seqlen_q < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || total_q < 0 ||
-      total_k < 0)
+                                  int64_t out_stride_head, void* workspace,
+                                  size_t workspace_bytes, int32_t dtype, void* stream) {
+  if (batch < 0 || max_seqlen_q < 0 || max_seqlen_k < 0 || num_q_heads <= 0 ||
+      num_kv_heads <= 0 || total_q < 0 || total_k < 0)
     return NVK_EINVAL;
   if (!(scale > 0.f)) return NVK_EINVAL;  // the row max is taken before scaling
   if (dtype != NVK_DTYPE_BF16) return NVK_EUNSUPPORTED;
@@ -576,6 +737,19 @@ extern "C" int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q
   if ((q_stride_tok % 8) || (q_stride_head % 8)) return NVK_EALIGN;
   if (((uintptr_t)out % 8) || (out_stride_tok % 4) || (out_stride_head % 4)) return NVK_EALIGN;
   if (batch > 65535) return NVK_EINVAL;
+  if (workspace && (uintptr_t)workspace % 256) return NVK_EALIGN;
+
+  // Keys per sequence are bounded by max_seqlen_k (when given) and by the table
+  // (paged) or the k rows (dense).
+  int64_t max_keys = block_tables ? (int64_t)max_blocks * block_size : total_k;
+  if (max_seqlen_k > 0 && max_seqlen_k < max_keys) max_keys = max_seqlen_k;
+  SplitPlan sp = plan_splits(batch, max_seqlen_q, max_keys, num_q_heads, num_kv_heads);
+  if (sp.n_qtiles > 65535) return NVK_EINVAL;
+  if (sp.n_splits > 1 && (!workspace || workspace_bytes < split_workspace_bytes(sp, batch,
+                                                                                num_kv_heads))) {
+    sp.n_splits = 1;  // no room for partials: one workgroup per query tile
+    sp.tiles_per_split = (int)((max_keys + kKeys - 1) / kKeys);
+  }
 
   PrefillArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -603,9 +777,10 @@ extern "C" int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q
   a.out = static_cast<uint16_t*>(out);
   a.out_stride_tok = out_stride_tok;
   a.out_stride_head = out_stride_head;
-  const int TQ = kRows / G;
-  a.n_qtiles = (max_seqlen_q + TQ - 1) / TQ;
-  if (a.n_qtiles > 65535) return NVK_EINVAL;
+  a.n_qtiles = sp.n_qtiles;
+  a.n_splits = sp.n_splits;
+  a.tiles_per_split = sp.n_splits > 1 ? sp.tiles_per_split : 1 << 30;
+  a.ws = static_cast<float*>(workspace);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (G) {
     case 1: return launch_prefill<1>(a, s);

@@ -34,11 +34,14 @@ def _int32(t: torch.Tensor) -> torch.Tensor:
 
 
 def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_scale,
-                   block_table=None, out=None):
+                   block_table=None, out=None, max_seqlen_k=None):
     """Causal varlen attention (bottom-right aligned), dense or paged keys.
 
     q: [Tq, Hq, D]; dense k/v: [Tk, Hkv, D]; paged k/v: [NB, bs, Hkv, D] caches
     with ``block_table`` [B, W] int32.  Returns [Tq, Hq, D] (or fills ``out``).
+    ``max_seqlen_k`` (host int, optional) bounds the keys of a sequence; the
+    library uses it to decide whether to split long key ranges across
+    workgroups (the workspace for that is allocated here, with torch).
     """
     dev = _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, block_table)
     _check_bf16(q, k, v)
@@ -75,14 +78,19 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_sc
         raise _lib.NvkError("q and k head_dim differ")
     scale = float(softmax_scale) if softmax_scale is not None else d ** -0.5
     lib = _lib.load()
+    key_bound = max_blocks * block_size if bt is not None else total_k
+    msk = min(int(max_seqlen_k), key_bound) if max_seqlen_k else key_bound
+    ws_bytes = lib.nvk_varlen_prefill_workspace_size(batch, int(max_seqlen_q), msk, hq, hkv, d)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     with torch.cuda.device(dev):
         code = lib.nvk_varlen_prefill(
             q.data_ptr(), q.stride(0), q.stride(1), tq,
             k.data_ptr(), v.data_ptr(), k_st, v_st, kv_sh, total_k,
-            cu_q.data_ptr(), cu_k.data_ptr(), batch, int(max_seqlen_q),
+            cu_q.data_ptr(), cu_k.data_ptr(), batch, int(max_seqlen_q), msk,
             _lib.ptr(bt), bt_stride, max_blocks, block_size, num_blocks,
             hq, hkv, d, scale,
             out.data_ptr(), out.stride(0), out.stride(1),
+            _lib.ptr(ws), ws_bytes,
             _lib.NVK_DTYPE_BF16, _lib.stream_ptr(dev))
     _lib.check(code)
     return out
@@ -133,7 +141,7 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
                  window_size=(tuple(window_size), (-1, -1)), softcap=(softcap, 0.0),
                  alibi_slopes=(alibi_slopes, None), return_attn_probs=(return_attn_probs, False))
     return varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_scale,
-                          block_table=block_table)
+                          block_table=block_table, max_seqlen_k=max_seqlen_k)
 
 
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None, rotary_sin=None,

@@ -69,7 +69,8 @@ class Attention(nn.Module):
             if context.block_tables is not None:    # prefix cache / later chunk
                 k, v = k_cache, v_cache
             o = varlen_prefill(q, k, v, context.cu_seqlens_q, context.cu_seqlens_k,
-                               context.max_seqlen_q, self.scale, block_table=context.block_tables)
+                               context.max_seqlen_q, self.scale, block_table=context.block_tables,
+                               max_seqlen_k=context.max_seqlen_k)
         else:    # decode
             o = paged_decode(q, k_cache, v_cache, context.context_lens, context.block_tables,
                              self.scale).unsqueeze(1)

@@ -68,8 +68,17 @@ def test_error_codes_without_launching():
     assert lib.nvk_paged_decode_workspace_size(1, 2, 1, 128, 64, 1) == 256 + 4 * 2 * 2 * 132 * 4
     assert lib.nvk_paged_decode_workspace_size(4, 16, 5, 128, 256, 1) == 0   # 16 % 5 != 0
     # prefill: head_dim 64 not built
-    assert lib.nvk_varlen_prefill(16, 2048, 128, 4, 16, 16, 1024, 1024, 128, 4, 16, 16, 1, 4, None,
-                                  0, 0, 0, 0, 16, 8, 64, 0.1, 16, 2048, 128, 0, None) == -2
+    assert lib.nvk_varlen_prefill(16, 2048, 128, 4, 16, 16, 1024, 1024, 128, 4, 16, 16, 1, 4, 4,
+                                  None, 0, 0, 0, 0, 16, 8, 64, 0.1, 16, 2048, 128, None, 0, 0,
+                                  None) == -2
+    # split-K workspace: 32 sequences of 6 queries over <= 8192 keys (8 kv heads x 32 x 1
+    # query tile = 256 workgroups) split 4 ways; records of 128 rows x (128 + 4) floats
+    assert lib.nvk_varlen_prefill_workspace_size(32, 6, 8192, 16, 8, 128) == \
+        8 * 32 * 1 * 4 * 128 * 132 * 4
+    # enough query tiles to fill the GPU: no split, no workspace
+    assert lib.nvk_varlen_prefill_workspace_size(32, 1024, 1536, 16, 8, 128) == 0
+    # short key ranges are never split
+    assert lib.nvk_varlen_prefill_workspace_size(1, 6, 512, 16, 8, 128) == 0
 
 
 def test_cpu_tensors_are_rejected_not_served():
