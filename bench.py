@@ -8,8 +8,14 @@ kernel and its combine pass).  `value` = algorithmic bytes of a step (unique
 K+V bytes of every context + q read + output written) / wall time per step,
 with every input resident in HBM.  Two more legs ride along in the same JSON
 line: the KV-store scatter (4096 tokens into a 64-page cache, 5 % slots -1)
-in GB/s and the varlen prefill over a 512-token shared prefix (32 sequences,
-U{100..1024} new tokens) in TFLOP/s of unmasked QK^T + PV work.
+in GB/s, the varlen prefill over a 512-token shared prefix (32 sequences,
+U{100..1024} new tokens) in TFLOP/s of unmasked QK^T + PV work, the
+speculative-decode verification (32 sequences, 6 queries over U{1024..8192}
+keys, split-K) in GB/s, and a mixed step of 28 layers (per layer: KV-store of
+4288 tokens, 8 prefill chunks of 512 after U{0..1536} cached tokens, 192
+decodes over U{256..4096}; a separate KV pool per layer) as the fraction of
+its roofline time (decode and store bytes at HBM peak + prefill FLOPs at MFMA
+peak).
 
 Timing: each leg builds K steps into one HIP graph (the decode steps cycle
 over four copies of the KV pool, so no step finds its working set in the
@@ -20,6 +26,10 @@ achieved).  The CPU baseline is the numpy oracle on one host thread, timed on
 the same inputs.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                  [--legs decode,store,prefill,spec,mixed] [--eager]
+
+--eager launches the steps one by one instead of replaying a graph (for
+counter collection with rocprofv3, which profiles individual dispatches).
 """
 from __future__ import annotations
 
@@ -46,8 +56,10 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--legs", default="decode,store,prefill",
-                   help="comma list of legs to run (decode is the headline)")
+    p.add_argument("--legs", default="decode,store,prefill,spec,mixed",
+                   help="comma list of legs to run (decode, the headline, always runs)")
+    p.add_argument("--eager", action="store_true",
+                   help="launch steps one by one (no graph), e.g. under rocprofv3 --pmc")
     return p.parse_args()
 
 
@@ -55,9 +67,27 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_graph(torch, step_fns, steps, warmup):
+def time_eager(torch, step_fns, steps, warmup):
+    """Launch `steps` calls (cycling over step_fns) one by one; return
+    (wall seconds per step, event seconds per step)."""
+    for i in range(max(1, warmup)):
+        step_fns[i % len(step_fns)]()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        step_fns[i % len(step_fns)]()
+    end.record()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps, start.elapsed_time(end) / 1e3 / steps
+
+
+def time_graph(torch, step_fns, steps, warmup, eager=False):
     """Capture `steps` calls (cycling over step_fns) in one graph; return
     (wall seconds per step, event seconds per step)."""
+    if eager:
+        return time_eager(torch, step_fns, steps, warmup)
     def capture(n):
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream()
@@ -104,6 +134,62 @@ def traffic_for(leg):
         return None
 
 
+def mixed_leg(torch, dev, args, orc, layers=28):
+    """28 layers of one mixed step, each with its own KV pool (random bf16 made on
+    the GPU) and the same block tables / slots; a layer = KV-store of every new
+    token, the prefill chunks, the decodes."""
+    from nanovllm_amd import paged_decode, store_kvcache, varlen_prefill
+    from nanovllm_amd.workloads import mixed_step_metadata
+
+    log(f"building mixed step ({layers} layers, ~3.5 GB of KV pool per layer)")
+    tens, meta = mixed_step_metadata()
+    t = {k: v.to(dev) for k, v in tens.items()}
+    gen = torch.Generator(device=dev).manual_seed(3)
+    rnd = lambda *shape: torch.randn(*shape, generator=gen, device=dev,
+                                     dtype=torch.float32).to(torch.bfloat16)
+    n_tok, nb = meta["n_tokens"], meta["pool_blocks"]
+    q_pf, q_dec = rnd(4096, 16, 128), rnd(192, 16, 128)
+    key, value = rnd(n_tok, 8, 128), rnd(n_tok, 8, 128)
+    pools = []
+    for _ in range(layers):
+        kc = torch.empty(nb, 256, 8, 128, dtype=torch.bfloat16, device=dev)
+        vc = torch.empty_like(kc)
+        for x in (kc, vc):
+            for i in range(0, nb, 256):
+                x[i:i + 256].copy_(rnd(min(256, nb - i), 256, 8, 128))
+        pools.append((kc, vc))
+    o_pf, o_dec = torch.empty_like(q_pf), torch.empty_like(q_dec)
+    scale = 128 ** -0.5
+
+    def step():
+        for kc, vc in pools:
+            store_kvcache(key, value, kc, vc, t["slot_mapping"])
+            varlen_prefill(q_pf, kc, vc, t["cu_seqlens_q"], t["cu_seqlens_k"],
+                           meta["max_seqlen_q"], scale, block_table=t["prefill_block_tables"],
+                           out=o_pf, max_seqlen_k=meta["max_seqlen_k"])
+            paged_decode(q_dec, kc, vc, t["context_lens"], t["decode_block_tables"], scale,
+                         out=o_dec)
+
+    steps, warm = min(args.steps, 10), min(args.warmup, 2)
+    log("timing mixed step")
+    wall, ev = time_graph(torch, [step], steps, warm, args.eager)
+    dec_bytes = orc.attention_bytes(meta["dec_lens"], 8, 128, 192, 16)
+    pf_flops = orc.prefill_flops(meta["lens_q"], meta["lens_k"], 16, 128)
+    st_bytes = int((tens["slot_mapping"] >= 0).sum()) * 2 * 2 * 2048 + 4 * n_tok
+    t_roof = layers * ((dec_bytes + st_bytes) / (HBM_PEAK_GBS * 1e9) +
+                       pf_flops / (BF16_PEAK_TFLOPS * 1e12))
+    del pools
+    return dict(ms_per_step=wall * 1e3, layers=layers, steps=steps,
+                workload="28 layers x (KV-store 4288 tokens + 8 prefill chunks of 512 after "
+                         "U{0..1536} cached + 192 decodes over U{256..4096}), 3300-page pool "
+                         "per layer",
+                per_layer={"decode_bytes": dec_bytes, "prefill_flops": pf_flops,
+                           "store_bytes": st_bytes},
+                roofline={"bound": "mixed", "t_roof_ms": round(t_roof * 1e3, 4),
+                          "t_measured_ms": round(ev * 1e3, 4),
+                          "frac": round(t_roof / ev, 4)})
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -117,7 +203,8 @@ def main():
     from threadpoolctl import threadpool_limits
 
     from nanovllm_amd import paged_decode, store_kvcache, varlen_prefill
-    from nanovllm_amd.workloads import decode_case, kv_store_case, prefill_case
+    from nanovllm_amd.workloads import (decode_case, kv_store_case, prefill_case,
+                                        spec_verify_case)
     from oracle import kv_oracle as orc
 
     legs = set(args.legs.split(","))
@@ -137,7 +224,7 @@ def main():
         for c, o in zip(pools, outs)]
     dec_bytes = orc.attention_bytes(dc.lens, 8, 128, 64, 16)
     log("timing decode")
-    wall, ev = time_graph(torch, dec_fns, args.steps, args.warmup)
+    wall, ev = time_graph(torch, dec_fns, args.steps, args.warmup, args.eager)
     dec_gbs = dec_bytes / wall / 1e9
     dec_ach = dec_bytes / ev / 1e9
     result["decode"] = dict(ms_per_step=wall * 1e3, gbs=dec_gbs, event_gbs=dec_ach,
@@ -165,7 +252,7 @@ def main():
         n_valid = int((sc.slot_mapping >= 0).sum())
         st_bytes = n_valid * 2 * 2 * 8 * 128 * 2 + 4 * 4096
         log("timing kv-store")
-        wall_s, ev_s = time_graph(torch, st_fns, args.steps, args.warmup)
+        wall_s, ev_s = time_graph(torch, st_fns, args.steps, args.warmup, args.eager)
         leg = dict(ms_per_step=wall_s * 1e3, bytes_per_step=st_bytes,
                    roofline={"bound": "hbm", "achieved": round(st_bytes / ev_s / 1e9, 2),
                              "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -200,7 +287,7 @@ def main():
                   for c, o in zip(copies, outs)]
         flops = orc.prefill_flops(pc.lens_q, pc.lens_k, 16, 128)
         log("timing prefill")
-        wall_p, ev_p = time_graph(torch, pf_fns, args.steps, args.warmup)
+        wall_p, ev_p = time_graph(torch, pf_fns, args.steps, args.warmup, args.eager)
         tf = flops / ev_p / 1e12
         leg = dict(ms_per_step=wall_p * 1e3, flops_per_step=flops,
                    roofline={"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
@@ -218,6 +305,37 @@ def main():
                                    "sample": "the full 32-sequence prefill through the numpy "
                                              "oracle, median of 3 reps on 1 host thread"}
         result["prefill"] = leg
+        del copies, outs, pf_fns
+
+    # ------------------------------------------------------------------ spec verify
+    if "spec" in legs:
+        log("building spec-verify workload (32 seqs, 6 queries, ctx U{1024..8192})")
+        vc_ = spec_verify_case()
+        copies = [vc_.to(dev) for _ in range(2)]
+        for c in copies:   # the 5 draft tokens of every sequence are stored first
+            store_kvcache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping)
+        outs = [torch.empty_like(c.q) for c in copies]
+        sv_fns = [(lambda c=c, o=o: varlen_prefill(c.q, c.k_cache, c.v_cache, c.cu_seqlens_q,
+                                                   c.cu_seqlens_k, vc_.max_seqlen_q, vc_.scale,
+                                                   block_table=c.block_tables, out=o,
+                                                   max_seqlen_k=vc_.max_seqlen_k))
+                  for c, o in zip(copies, outs)]
+        sv_bytes = orc.attention_bytes(vc_.lens_k, 8, 128, 32 * 6, 16)
+        log("timing spec verify")
+        wall_v, ev_v = time_graph(torch, sv_fns, args.steps, args.warmup, args.eager)
+        result["spec_verify"] = dict(
+            ms_per_step=wall_v * 1e3, bytes_per_step=sv_bytes,
+            workload="32 sequences x 6 query tokens (5 drafts + the last accepted token) over "
+                     "U{1024..8192} paged keys, split-K",
+            roofline={"bound": "hbm", "achieved": round(sv_bytes / ev_v / 1e9, 2),
+                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(sv_bytes / ev_v / 1e9 / HBM_PEAK_GBS, 4),
+                      "traffic": traffic_for("spec_verify")})
+        del copies, outs, sv_fns
+
+    # ------------------------------------------------------------------ mixed step
+    if "mixed" in legs:
+        result["mixed_step"] = mixed_leg(torch, dev, args, orc)
 
     d = result["decode"]
     line = {
@@ -243,7 +361,7 @@ def main():
                      "traffic": traffic_for("decode")},
         "cpu_baseline": cpu,
     }
-    for k in ("kv_store", "prefill"):
+    for k in ("kv_store", "prefill", "spec_verify", "mixed_step"):
         if k in result:
             line[k] = result[k]
     print(json.dumps(line), flush=True)

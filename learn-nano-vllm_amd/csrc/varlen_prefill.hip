@@ -370,8 +370,10 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
     const float mt = nvk_max_xor32(mx) * a.scale_log2;
     const bool need = mt > m_ref + kLazy;
     if (__builtin_amdgcn_ballot_w64(need)) {
+      // Lanes that do not need it keep alpha = 1 (a row with no visible key so
+      // far has m_ref = -inf, and exp2(-inf - -inf) would be NaN).
       const float m_new = need ? mt : m_ref;
-      const float alpha = nvk_fast_exp2(m_ref - m_new);  // 0 when m_ref = -inf
+      const float alpha = need ? nvk_fast_exp2(m_ref - m_new) : 1.f;  // 0 when m_ref = -inf
       m_ref = m_new;
 #pragma unroll
       for (int j = 0; j < 2; ++j) l_part[j] *= alpha;

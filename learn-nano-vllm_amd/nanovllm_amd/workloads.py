@@ -172,12 +172,11 @@ def spec_verify_case(seed=4, batch=32, n_query=6, n_draft=5, ctx_lo=1024, ctx_hi
                      lens_k=lens, max_seqlen_q=n_query, max_seqlen_k=max(lens), tables=tables))
 
 
-def mixed_layer_case(seed=3, n_chunks=8, chunk=512, cached_lo=0, cached_hi=1536, n_decode=192,
-                     ctx_lo=256, ctx_hi=4096, hq=HQ, hkv=HKV, hd=HD, block_size=BLOCK,
-                     pool_blocks=3300):
-    """One layer of a mixed step: prefill chunks (paged, mid-page starts allowed)
-    and decode sequences share one cache pool."""
-    gen = torch.Generator().manual_seed(seed)
+def mixed_step_metadata(seed=3, n_chunks=8, chunk=512, cached_lo=0, cached_hi=1536, n_decode=192,
+                        ctx_lo=256, ctx_hi=4096, block_size=BLOCK, pool_blocks=3300, gen=None):
+    """Block tables, slots and lengths of one mixed step (shared by every layer):
+    prefill chunks (paged, mid-page starts allowed) and decodes in one pool."""
+    gen = gen if gen is not None else torch.Generator().manual_seed(seed)
     cached = _randint(gen, cached_lo, cached_hi, n_chunks)
     dec_lens = _randint(gen, ctx_lo, ctx_hi, n_decode)
     perm = torch.randperm(pool_blocks, generator=gen).tolist()
@@ -199,20 +198,33 @@ def mixed_layer_case(seed=3, n_chunks=8, chunk=512, cached_lo=0, cached_hi=1536,
         dec_tables.append(t)
         dec_slots.append(t[(n - 1) // block_size] * block_size + (n - 1) % block_size)
     assert nxt <= pool_blocks, "pool too small"
+    lens_k = [c + chunk for c in cached]
+    cu_q = torch.arange(0, (n_chunks + 1) * chunk, chunk, dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(torch.tensor(lens_k).cumsum(0).tolist()), dtype=torch.int32)
+    return dict(slot_mapping=torch.tensor(pf_slots + dec_slots, dtype=torch.int32),
+                prefill_block_tables=_pad_tables(pf_tables), cu_seqlens_q=cu_q,
+                cu_seqlens_k=cu_k, decode_block_tables=_pad_tables(dec_tables),
+                context_lens=torch.tensor(dec_lens, dtype=torch.int32)), \
+        dict(block_size=block_size, lens_q=[chunk] * n_chunks, lens_k=lens_k, max_seqlen_q=chunk,
+             max_seqlen_k=max(lens_k), dec_lens=dec_lens, n_tokens=n_chunks * chunk + n_decode,
+             pool_blocks=pool_blocks)
+
+
+def mixed_layer_case(seed=3, n_chunks=8, chunk=512, cached_lo=0, cached_hi=1536, n_decode=192,
+                     ctx_lo=256, ctx_hi=4096, hq=HQ, hkv=HKV, hd=HD, block_size=BLOCK,
+                     pool_blocks=3300):
+    """One layer of a mixed step: prefill chunks (paged, mid-page starts allowed)
+    and decode sequences share one cache pool."""
+    gen = torch.Generator().manual_seed(seed)
+    tensors, meta = mixed_step_metadata(seed, n_chunks, chunk, cached_lo, cached_hi, n_decode,
+                                        ctx_lo, ctx_hi, block_size, pool_blocks, gen=gen)
     tq = n_chunks * chunk
     q_pf = _randn(gen, tq, hq, hd)
     q_dec = _randn(gen, n_decode, hq, hd)
     key = _randn(gen, tq + n_decode, hkv, hd)
     value = _randn(gen, tq + n_decode, hkv, hd)
     k_cache, v_cache = _fill_pool(gen, pool_blocks, block_size, hkv, hd)
-    lens_k = [c + chunk for c in cached]
-    cu_q = torch.arange(0, (n_chunks + 1) * chunk, chunk, dtype=torch.int32)
-    cu_k = torch.tensor([0] + list(torch.tensor(lens_k).cumsum(0).tolist()), dtype=torch.int32)
-    return Case(dict(q_prefill=q_pf, q_decode=q_dec, key=key, value=value, k_cache=k_cache,
-                     v_cache=v_cache,
-                     slot_mapping=torch.tensor(pf_slots + dec_slots, dtype=torch.int32),
-                     prefill_block_tables=_pad_tables(pf_tables), cu_seqlens_q=cu_q,
-                     cu_seqlens_k=cu_k, decode_block_tables=_pad_tables(dec_tables),
-                     context_lens=torch.tensor(dec_lens, dtype=torch.int32)),
-                dict(block_size=block_size, scale=hd ** -0.5, lens_q=[chunk] * n_chunks,
-                     lens_k=lens_k, max_seqlen_q=chunk, dec_lens=dec_lens))
+    tensors.update(q_prefill=q_pf, q_decode=q_dec, key=key, value=value, k_cache=k_cache,
+                   v_cache=v_cache)
+    meta.update(scale=hd ** -0.5)
+    return Case(tensors, meta)

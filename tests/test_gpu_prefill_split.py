@@ -117,3 +117,12 @@ def test_split_dense_keys_and_empty_query_ranges():
     ref = oracle_prefill_dense(q, k, v, cu_q, cu_k, 0.09)
     assert_attn_close(split, ref, "dense split")
     assert_attn_close(whole, ref, "dense unsplit")
+
+
+def test_split_where_most_rows_of_a_wave_see_no_key_of_the_split():
+    # 513 queries over 769 keys: the query tile of tokens 193..256 splits into keys
+    # 0..511 and 512..575, and of the last wave's rows only token 256 sees key 512;
+    # the other rows' partial for that split must stay empty (regression: the
+    # lazy-rescale factor of such rows was exp2(-inf - -inf) = NaN)
+    # (max_seqlen_k = the table's 4 pages, as when the caller gives no bound)
+    _check_paged(38, [513], [769], max_k=1024, what="rows without keys in a split")
