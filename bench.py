@@ -30,6 +30,9 @@ the same inputs.
 
 --eager launches the steps one by one instead of replaying a graph (for
 counter collection with rocprofv3, which profiles individual dispatches).
+--copy-calibration MiB only runs a plain device-to-device copy of that size
+(5 launches) and exits: the reference kernel of known traffic against which
+the HBM counters (FETCH_SIZE / WRITE_SIZE) of the legs are scaled.
 """
 from __future__ import annotations
 
@@ -60,6 +63,8 @@ def parse_args():
                    help="comma list of legs to run (decode, the headline, always runs)")
     p.add_argument("--eager", action="store_true",
                    help="launch steps one by one (no graph), e.g. under rocprofv3 --pmc")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
+                   help="only run a plain device copy of MiB mebibytes (counter calibration)")
     return p.parse_args()
 
 
@@ -201,6 +206,16 @@ def main():
     import numpy as np
     import torch
     from threadpoolctl import threadpool_limits
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
+        return
 
     from nanovllm_amd import paged_decode, store_kvcache, varlen_prefill
     from nanovllm_amd.workloads import (decode_case, kv_store_case, prefill_case,

@@ -653,10 +653,11 @@ int launch_prefill(const PrefillArgs& a, hipStream_t stream) {
 }
 
 
-// Split-K plan for a launch: split the key range when the query tiles alone
-// give fewer than ~4 workgroups per CU, keeping at least 8 key tiles (512
-// keys) per split.  Deterministic in its arguments, so the workspace query
-// and the launch agree.
+// Split-K plan for a launch: split the key range when the query ranges are
+// short (at most half a query tile, so partial records stay small next to the
+// keys they summarise) and the query tiles alone give fewer than ~4
+// workgroups per CU, keeping at least 8 key tiles (512 keys) per split.
+// Deterministic in its arguments, so the workspace query and the launch agree.
 struct SplitPlan {
   int n_qtiles, n_splits, tiles_per_split;
 };
@@ -670,7 +671,8 @@ static SplitPlan plan_splits(int batch, int max_seqlen_q, int64_t max_keys, int 
   const int64_t max_tiles = (max_keys + kKeys - 1) / kKeys;
   const int64_t wgs = (int64_t)num_kv_heads * batch * p.n_qtiles;
   constexpr int64_t kTargetWgs = 1024, kMinTilesPerSplit = 8, kMaxSplits = 16;
-  if (wgs > 0 && wgs < kTargetWgs && max_tiles >= 2 * kMinTilesPerSplit) {
+  if (wgs > 0 && wgs < kTargetWgs && max_tiles >= 2 * kMinTilesPerSplit &&
+      2 * max_seqlen_q <= TQ) {
     int64_t n = (kTargetWgs + wgs - 1) / wgs;
     if (n > max_tiles / kMinTilesPerSplit) n = max_tiles / kMinTilesPerSplit;
     if (n > kMaxSplits) n = kMaxSplits;
