@@ -38,8 +38,10 @@
 namespace {
 
 constexpr int HD = 128;
-constexpr int kWaves = 4;
-constexpr int kRows = 128;                   // query rows per workgroup
+constexpr int kWaves = 4;                    // waves per workgroup
+constexpr int kRows = 32 * kWaves;           // query rows per workgroup (32 per wave)
+constexpr int kTileRowsPerWave = 64 / kWaves;      // key rows of a tile each wave loads
+constexpr int kLoadsPerWave = kTileRowsPerWave / 4;  // 4-row (1 KiB) loads per wave
 constexpr int kKeys = 64;                    // keys per tile
 constexpr int kRowBytes = HD * 2;            // LDS bytes of one key row
 constexpr int kTileBytes = kKeys * kRowBytes;
@@ -141,15 +143,16 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // them; completion is awaited explicitly (vmcnt) before the publishing barrier.
 // `rsrc`: a raw buffer descriptor (wave-uniform); loads at offsets >= its
 // size write zeros.
-// The descriptor and the LDS address are wave-uniform; readfirstlane puts
-// them in SGPRs where the compiler computed them with vector instructions.
+// `rsrc` and `dst` must be wave-uniform values held in SGPRs (see uniform()).
 __device__ __forceinline__ void lds_load_buffer(const nvk_u32x4& rsrc, uint32_t voffset,
                                                 uint32_t dst) {
-  auto u = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); };
-  const nvk_u32x4 r = {u(rsrc.x), u(rsrc.y), u(rsrc.z), u(rsrc.w)};
   asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :: "v"(voffset), "s"(r), "s"((uint32_t)__builtin_amdgcn_readfirstlane((int)dst))
-               : "memory", "m0");
+               :: "v"(voffset), "s"(rsrc), "s"(dst) : "memory", "m0");
+}
+// readfirstlane of wave-uniform values the compiler may have computed with
+// vector instructions (inline asm "s" operands need SGPRs).
+__device__ __forceinline__ uint32_t uniform(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
 }
 __device__ __forceinline__ void lds_load_global(const void* src, uint32_t dst) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
@@ -160,7 +163,7 @@ __device__ __forceinline__ void wait_lds_loads() {
 }
 
 template <int G, int MODE>
-__global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel(PrefillArgs a) {
   constexpr int TQ = kRows / G;  // query tokens per workgroup
 
   const int kvh = blockIdx.x;
@@ -213,11 +216,14 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   const int row_limit = tok + diag;  // last visible key of this row
 
   // ---- tile loads straight into LDS ---------------------------------------------
-  // Wave w fills rows 16w..16w+15 of a stage with 4 loads of 4 rows; lane l
-  // writes LDS chunk l of the load, i.e. row 16w + 4j + l/16, slot l%16, so
-  // it fetches chunk (l%16) ^ swz(row) of that key row.
+  // Wave w fills its kTileRowsPerWave rows of a stage (64 / kWaves, from row
+  // w*kTileRowsPerWave) with loads of 4 rows; lane l writes LDS chunk l of
+  // load j, i.e. row w*kTileRowsPerWave + 4j + l/16, slot l%16, so it fetches
+  // chunk (l%16) ^ swz(row) of that key row.
   const int dma_rsub = lane >> 4;  // row within the 4-row block
-  auto dma_chunk = [&](int j) { return (lane & 15) ^ ((dma_rsub << 2) | j); };
+  // first tile row of the wave's load j, and the chunk this lane fetches for it
+  auto dma_row0 = [&](int j) { return kTileRowsPerWave * wave + 4 * j; };
+  auto dma_chunk = [&](int j) { return (lane & 15) ^ ((dma_rsub << 2) | ((dma_row0(j) >> 2) & 3)); };
   const uint32_t k_row_bytes =
       MODE == kDense ? (uint32_t)a.k_stride_tok * 2u : (uint32_t)a.num_kv_heads * HD * 2u;
   const uint32_t v_row_bytes =
@@ -228,63 +234,64 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   const uint16_t* dummy = a.q + (int64_t)q_row0 * a.q_stride_tok;
 
   // A K or V tile load into one LDS stage, planned once per tile and issued as
-  // 4 instructions (load j fills rows 16w+4j .. +3 of the wave's quarter), so
-  // the issues can be spread over the MFMA work.  Dense / aligned paged: one
-  // buffer descriptor per load over the valid rows only (rows past them load
-  // zeros); a tile that does not exist has 0 valid rows.  kPagedAny: per-row
+  // kLoadsPerWave instructions per wave (load j: 4 rows), so the issues can be
+  // spread over the MFMA work.  Dense / aligned paged: one buffer descriptor
+  // over the tile's valid rows (rows past them load zeros; a tile that does
+  // not exist has none), lane offsets fixed per load.  kPagedAny: per-row
   // global addresses, resolved when the plan is made.
   struct DmaPlan {
-    const uint16_t* tb;    // row 0 of the tile (head kvh)
-    int bytes;             // valid bytes from tb (rows * row_bytes)
-    uint32_t row_bytes;
-    uint32_t dst0;         // LDS byte address of the wave's first row
-    const uint16_t* rows[4];  // kPagedAny: this lane's source per load
+    nvk_u32x4 rsrc;                       // SGPRs
+    uint32_t dst0;                        // LDS byte address of the wave's first row
+    const uint16_t* rows[kLoadsPerWave];  // kPagedAny: this lane's source per load
   };
-  auto plan_tile = [&](int kt, uint8_t* dst, bool is_v, int page) {
+  uint32_t k_voff[kLoadsPerWave], v_voff[kLoadsPerWave];  // lane byte offset of load j
+#pragma unroll
+  for (int j = 0; j < kLoadsPerWave; ++j) {
+    k_voff[j] = (uint32_t)(dma_row0(j) + dma_rsub) * k_row_bytes + 16u * (uint32_t)dma_chunk(j);
+    v_voff[j] = (uint32_t)(dma_row0(j) + dma_rsub) * v_row_bytes + 16u * (uint32_t)dma_chunk(j);
+  }
+  // `page` / `in_page` (kPagedAligned): the tile's page id and its first key's
+  // offset inside that page (multiples of 64, kept by the caller without
+  // divisions).
+  auto plan_tile = [&](int kt, uint8_t* dst, bool is_v, int page, int in_page) {
     DmaPlan pl;
     const int base = kt * kKeys;
     const uint16_t* src = is_v ? a.v : a.k;
-    pl.dst0 = lds_addr(dst + 16 * wave * kRowBytes);
-    pl.row_bytes = is_v ? v_row_bytes : k_row_bytes;
+    pl.dst0 = uniform(lds_addr(dst + kTileRowsPerWave * wave * kRowBytes));
     int rem = n_keys - base < kKeys ? n_keys - base : kKeys;
     rem = (rem > 0 && kt < t_end) ? rem : 0;
     if constexpr (MODE == kPagedAny) {
-      pl.tb = src;
-      pl.bytes = 0;
+      pl.rsrc = nvk_u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int pos = base + 16 * wave + 4 * j + dma_rsub;
+      for (int j = 0; j < kLoadsPerWave; ++j) {
+        const int pos = base + dma_row0(j) + dma_rsub;
         const int64_t prow = pos < n_keys ? nvk_paged_row(bt_row, pos, a.block_size, a.bs_shift,
                                                           a.num_blocks) : -1;
         pl.rows[j] = (prow >= 0 ? src + prow * paged_row_elems + kvh * HD : dummy) +
                      8 * dma_chunk(j);
       }
     } else {
-      pl.bytes = rem * (int)pl.row_bytes;
+      const uint16_t* tb;
+      uint32_t bytes = (uint32_t)rem * (is_v ? v_row_bytes : k_row_bytes);
       if constexpr (MODE == kDense) {
-        pl.tb = src + (int64_t)(k_row0 + base) * (is_v ? a.v_stride_tok : a.k_stride_tok) +
-                (int64_t)kvh * a.kv_stride_head;
+        tb = src + (int64_t)(k_row0 + base) * (is_v ? a.v_stride_tok : a.k_stride_tok) +
+             (int64_t)kvh * a.kv_stride_head;
       } else {
-        const int logical = a.bs_shift >= 0 ? base >> a.bs_shift : base / a.block_size;
-        const int64_t prow = (int64_t)page * a.block_size + (base - logical * a.block_size);
-        const bool ok = (uint32_t)page < (uint32_t)a.num_blocks && rem > 0;
-        pl.tb = ok ? src + prow * paged_row_elems + kvh * HD : src;
-        pl.bytes = ok ? pl.bytes : 0;
+        const bool ok = (uint32_t)page < (uint32_t)a.num_blocks;
+        const int64_t prow = ok ? (int64_t)page * a.block_size + in_page : 0;  // no branch
+        tb = src + prow * paged_row_elems + kvh * HD;
+        bytes = ok ? bytes : 0u;
       }
+      const nvk_u32x4 r = tile_rsrc(tb, bytes);
+      pl.rsrc = nvk_u32x4{uniform(r.x), uniform(r.y), uniform(r.z), uniform(r.w)};
     }
     return pl;
   };
-  auto issue_load = [&](const DmaPlan& pl, int j) {
-    if constexpr (MODE == kPagedAny) {
+  auto issue_load = [&](const DmaPlan& pl, int j, bool is_v) {
+    if constexpr (MODE == kPagedAny)
       lds_load_global(pl.rows[j], pl.dst0 + 4 * j * kRowBytes);
-    } else {
-      const int skip = (16 * wave + 4 * j) * (int)pl.row_bytes;
-      int left = pl.bytes - skip;
-      left = left > 0 ? left : 0;
-      const uint32_t voff = (uint32_t)dma_rsub * pl.row_bytes +
-                            16u * (uint32_t)((lane & 15) ^ ((dma_rsub << 2) | j));
-      lds_load_buffer(tile_rsrc(pl.tb + skip / 2, (uint32_t)left), voff, pl.dst0 + 4 * j * kRowBytes);
-    }
+    else
+      lds_load_buffer(pl.rsrc, is_v ? v_voff[j] : k_voff[j], pl.dst0 + 4 * j * kRowBytes);
   };
 
   // Page ids (kPagedAligned): read one step before the tile's load is issued.
@@ -346,11 +353,10 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   float m_ref = -INFINITY;
   float l_part[2] = {0.f, 0.f};  // this lane's share of the row sum (two chains)
 
-  // Masks the tile (boundary tiles only), takes its row max and rescales when
-  // the max moved past the headroom; returns the offset for exp2.
-  auto softmax_max = [&](nvk_f32x16 (&sc)[2], int kt) -> float {
+  // Scores of keys a row may not see -> -inf (boundary tiles only; uniform).
+  auto mask_tile = [&](nvk_f32x16 (&sc)[2], int kt) {
     const int kbase = kt * kKeys;
-    if (kbase + kKeys > unmasked_keys || kbase + kKeys > n_keys) {  // uniform
+    if (kbase + kKeys > unmasked_keys || kbase + kKeys > n_keys) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
@@ -360,14 +366,20 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
         }
       }
     }
-    float mx = nvk_max3(sc[0][0], sc[0][1], sc[0][2]);
-#pragma unroll
-    for (int i = 3; i < 15; i += 2) mx = nvk_max3(mx, sc[0][i], sc[0][i + 1]);
-    mx = nvk_max3(mx, sc[0][15], sc[1][0]);
-#pragma unroll
-    for (int i = 1; i < 15; i += 2) mx = nvk_max3(mx, sc[1][i], sc[1][i + 1]);
-    mx = fmaxf(mx, sc[1][15]);
-    const float mt = nvk_max_xor32(mx) * a.scale_log2;
+  };
+  // Row max of a tile as a chain of 15 v_max3 steps (step 0 takes scores 0-2,
+  // step st > 0 scores 2st+1 and 2st+2) and a final max with score 31, so the
+  // steps can be spread over MFMAs; score i of the 32 is sc[i / 16][i % 16].
+  auto max_step = [&](const nvk_f32x16 (&sc)[2], float mx, int st) -> float {
+    auto v = [&](int i) { return sc[i >> 4][i & 15]; };
+    return st == 0 ? nvk_max3(v(0), v(1), v(2)) : nvk_max3(mx, v(2 * st + 1), v(2 * st + 2));
+  };
+  auto max_finish = [&](const nvk_f32x16 (&sc)[2], float mx) -> float {
+    return nvk_max_xor32(fmaxf(mx, sc[1][15])) * a.scale_log2;  // tile max, log2 units
+  };
+  // Lazy rescale for a tile whose row max (log2 units) is mt; returns the
+  // offset for exp2.
+  auto rescale = [&](float mt) -> float {
     const bool need = mt > m_ref + kLazy;
     if (__builtin_amdgcn_ballot_w64(need)) {
       // Lanes that do not need it keep alpha = 1 (a row with no visible key so
@@ -390,8 +402,10 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
     const int mb = p >> 1, i = 8 * (p & 1) + 2 * e;
     const float p0 = nvk_fast_exp2(fmaf(sc[mb][i], a.scale_log2, -moff));
     const float p1 = nvk_fast_exp2(fmaf(sc[mb][i + 1], a.scale_log2, -moff));
-    const uint32_t w = nvk_pack_bf16x2(p0, p1);
+    uint32_t w = nvk_pack_bf16x2(p0, p1);
     l_part[e & 1] = nvk_dot2_bf16(w, kOnes, l_part[e & 1]);
+    // keep this word where it is placed among the MFMAs (no sinking to its use)
+    asm volatile("" : "+v"(w), "+v"(l_part[e & 1]));
     return w;
   };
 
@@ -399,14 +413,19 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
   // fences keep the order; the compiler would otherwise group the MFMAs).
   // P fragment f holds keys 16f..16f+15 of tile kt; fragments 0-1 come from
   // score block 0, fragments 2-3 from block 1.  Order:
-  //   exp2 of fragment 0;  O k-step 0 (4 MFMAs) with the exp2 of fragment 1;
+  //   exp2 of fragment 0;
+  //   O k-step 0 (4 MFMAs) with the exp2 of fragment 1;
   //   S(kt+1) block 0 (8 MFMAs, into the consumed score block 0) with the
-  //   exp2 of fragments 2-3;  S(kt+1) block 1 (8);  O k-steps 1-3 (12).
-  // Ending on O MFMAs lets the next step's row max find S(kt+1) complete.
-  // The loads of V(kt+1) and K(kt+2) are issued between the MFMAs; LDS
-  // operands are read two MFMAs ahead.
+  //     exp2 of fragments 2-3;
+  //   S(kt+1) block 1 (8);
+  //   mask of S(kt+1) (boundary tiles only);
+  //   O k-steps 1-3 (12) with the row max of S(kt+1).
+  // Between the MFMAs: the loads of V(kt+1) and K(kt+2) and, in SALU, the
+  // plans of the next step's loads (V(kt+2), K(kt+3); pages pg_v / pg_k).
+  // LDS operands are read two MFMAs ahead.
   auto mma_step = [&](int kt, nvk_f32x16 (&sc)[2], float moff, const DmaPlan& plan_v,
-                      const DmaPlan& plan_k) {
+                      const DmaPlan& plan_k, int pg_v, int ip_v, int pg_k, int ip_k,
+                      DmaPlan& next_v, DmaPlan& next_k, float& mt_next) {
     uint32_t ka = k_addr0 + ((kt + 1) & 1) * kTileBytes;
     uint32_t va_lo = v_lo0 + (kt & 1) * kTileBytes, va_hi = v_hi0 + (kt & 1) * kTileBytes;
     asm volatile("" : "+v"(ka), "+v"(va_lo), "+v"(va_hi));  // rebuilt per step
@@ -427,6 +446,19 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
     auto pack = [](const uint32_t (&w)[4]) {
       return __builtin_bit_cast(nvk_bf16x8, nvk_u32x4{w[0], w[1], w[2], w[3]});
     };
+    // loads of this step: V(kt+1) during the O MFMAs, K(kt+2) during the S MFMAs
+    auto v_load_at = [&](int idx) {  // O MFMA index -> load number or -1
+      constexpr int kAt[4] = {1, 3, 5, 9};
+      for (int j = 0; j < kLoadsPerWave; ++j)
+        if (kAt[kLoadsPerWave > 2 ? j : 2 * j] == idx) return j;
+      return -1;
+    };
+    auto k_load_at = [&](int i) {  // S MFMA index (0..15) -> load number or -1
+      constexpr int kAt[4] = {2, 6, 10, 14};
+      for (int j = 0; j < kLoadsPerWave; ++j)
+        if (kAt[kLoadsPerWave > 2 ? j : 2 * j] == i) return j;
+      return -1;
+    };
     nvk_bf16x8 pf[4];
     uint32_t pw[4], pw3[4];
     nvk_bf16x8 vf[3];
@@ -436,113 +468,140 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
     for (int e = 0; e < 4; ++e) pw[e] = exp_word(sc, moff, 0, e);
     pf[0] = pack(pw);
     __builtin_amdgcn_sched_barrier(0);
-    // O k-step 0 with fragment 1.
     constexpr int kO = (kKeys / 16) * (HD / 32);
     auto o_mfma = [&](int idx) {  // idx = ks*4 + db; reads V two MFMAs ahead
       const int ks = idx / (HD / 32), db = idx % (HD / 32);
       if (idx + 2 < kO) vf[(idx + 2) % 3] = rd_v((idx + 2) % (HD / 32), (idx + 2) / (HD / 32));
       __builtin_amdgcn_sched_barrier(0);
       acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[idx % 3], pf[ks], acc_o[db], 0, 0, 0);
+      const int j = v_load_at(idx);
+      if (j >= 0) issue_load(plan_v, j, true);
     };
+    // O k-step 0 with fragment 1.
 #pragma unroll
     for (int idx = 0; idx < 4; ++idx) {
       o_mfma(idx);
       pw[idx] = exp_word(sc, moff, 1, idx);
-      if (idx == 1) issue_load(plan_v, 0);
-      if (idx == 3) issue_load(plan_v, 1);
       __builtin_amdgcn_sched_barrier(0);
     }
     pf[1] = pack(pw);
-    // S(kt+1): block 0 with fragments 2-3, then block 1.  After the last tile
-    // this multiplies a stale (or zero-filled) K stage; the result is unused.
-    {
-      nvk_bf16x8 kf[3];
-      kf[0] = rd_k(0, 0);
-      kf[1] = rd_k(1, 0);
-      sc[0] = nvk_f32x16{};
+    // S(kt+1), block 0 then block 1.  After the last tile this multiplies a
+    // stale (or zero-filled) K stage; the result is unused.
+    nvk_bf16x8 kf[3];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      kf[0] = rd_k(0, mb);
+      kf[1] = rd_k(1, mb);
+      sc[mb] = nvk_f32x16{};
 #pragma unroll
       for (int ks = 0; ks < HD / 16; ++ks) {
-        if (ks + 2 < HD / 16) kf[(ks + 2) % 3] = rd_k(ks + 2, 0);
+        if (ks + 2 < HD / 16) kf[(ks + 2) % 3] = rd_k(ks + 2, mb);
         __builtin_amdgcn_sched_barrier(0);
-        sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % 3], qf[ks], sc[0], 0, 0, 0);
-        if (ks < 4) pw[ks] = exp_word(sc, moff, 2, ks);
-        else pw3[ks - 4] = exp_word(sc, moff, 3, ks - 4);
-        if (ks == 2) issue_load(plan_k, 0);
-        if (ks == 6) issue_load(plan_k, 1);
+        sc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % 3], qf[ks], sc[mb], 0, 0, 0);
+        if (mb == 0) {
+          if (ks < 4) pw[ks] = exp_word(sc, moff, 2, ks);
+          else pw3[ks - 4] = exp_word(sc, moff, 3, ks - 4);
+        }
+        const int j = k_load_at(8 * mb + ks);
+        if (j >= 0) issue_load(plan_k, j, false);
+        if constexpr (MODE != kPagedAny) {
+          if (mb == 0 && ks == 5) next_v = plan_tile(kt + 2, v_stage(kt & 1), true, pg_v, ip_v);
+          if (mb == 1 && ks == 1)
+            next_k = plan_tile(kt + 3, k_stage((kt + 1) & 1), false, pg_k, ip_k);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
-      pf[2] = pack(pw);
-      pf[3] = pack(pw3);
-      kf[0] = rd_k(0, 1);
-      kf[1] = rd_k(1, 1);
-      sc[1] = nvk_f32x16{};
-#pragma unroll
-      for (int ks = 0; ks < HD / 16; ++ks) {
-        if (ks + 2 < HD / 16) kf[(ks + 2) % 3] = rd_k(ks + 2, 1);
-        __builtin_amdgcn_sched_barrier(0);
-        sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % 3], qf[ks], sc[1], 0, 0, 0);
-        if (ks == 2) issue_load(plan_k, 2);
-        if (ks == 6) issue_load(plan_k, 3);
-        __builtin_amdgcn_sched_barrier(0);
+      if (mb == 0) {
+        pf[2] = pack(pw);
+        pf[3] = pack(pw3);
       }
     }
-    // O k-steps 1-3.
+    mask_tile(sc, kt + 1);
+    // O k-steps 1-3 with the row max of S(kt+1) (15 max3 steps over 8 MFMAs).
+    float mx = 0.f;
 #pragma unroll
     for (int idx = 4; idx < kO; ++idx) {
       o_mfma(idx);
-      if (idx == 5) issue_load(plan_v, 2);
-      if (idx == 9) issue_load(plan_v, 3);
+      if (idx < 12) {
+        mx = max_step(sc, mx, 2 * (idx - 4));
+        if (2 * (idx - 4) + 1 < 15) mx = max_step(sc, mx, 2 * (idx - 4) + 1);
+      }
+      if (idx == 12) mt_next = max_finish(sc, mx);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
   // ---- pipelined main loop ------------------------------------------------------
-  // Step kt (one barrier): S(kt) is in registers, V(kt) and K(kt+1) are in
-  // LDS.  The step loads V(kt+1) into V stage (kt+1)&1 and K(kt+2) into K
-  // stage kt&1 while it computes O += V(kt) P(kt) and S(kt+1).  The barrier at
-  // the top of a step publishes the previous step's loads (each wave waits for
-  // its own first) and guarantees that every wave has finished reading the
-  // stages this step's loads overwrite.
-  int page_k = 0;      // kPagedAligned: page of tile kt+2 (read one step early)
-  int page_prev = 0;   // page of tile kt+1
+  // Step kt (one barrier): S(kt) and its row max are in registers, V(kt) and
+  // K(kt+1) are in LDS.  The step loads V(kt+1) into V stage (kt+1)&1 and
+  // K(kt+2) into K stage kt&1 while it computes O += V(kt) P(kt) and S(kt+1).
+  // The barrier at the top of a step publishes the previous step's loads
+  // (each wave waits for its own first) and guarantees that every wave has
+  // finished reading the stages this step's loads overwrite.  Page ids
+  // (aligned paged mode) are read two steps before their tile's plan.
   if (t_begin < t_end) {
     nvk_f32x16 sc[2];
     const int tb = t_begin;
-    int p0 = 0, p1 = 0;
+    int pg[4] = {0, 0, 0, 0};  // pages of tiles tb .. tb+3
+    int ip[4] = {0, 0, 0, 0};  // and their first keys' offsets in those pages
     if constexpr (MODE == kPagedAligned) {
-      p0 = __builtin_amdgcn_readfirstlane(fetch_page(tb));
-      p1 = tb + 1 < t_end ? __builtin_amdgcn_readfirstlane(fetch_page(tb + 1)) : 0;
-      if (tb + 2 < t_end) page_k = fetch_page(tb + 2);
-      page_prev = p1;
-    }
-    {
-      const DmaPlan k0 = plan_tile(tb, k_stage(tb & 1), false, p0);
-      const DmaPlan v0 = plan_tile(tb, v_stage(tb & 1), true, p0);
-      const DmaPlan k1 = plan_tile(tb + 1, k_stage((tb + 1) & 1), false, p1);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        issue_load(k0, j);
-        issue_load(v0, j);
-        issue_load(k1, j);
+      for (int i = 0; i < 4; ++i) pg[i] = fetch_page(tb + i);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pg[i] = __builtin_amdgcn_readfirstlane(pg[i]);
+        ip[i] = ((tb + i) * kKeys) % a.block_size;
       }
     }
+    auto next_in_page = [&](int x) { return x + kKeys == a.block_size ? 0 : x + kKeys; };
+    {
+      const DmaPlan k0 = plan_tile(tb, k_stage(tb & 1), false, pg[0], ip[0]);
+      const DmaPlan v0 = plan_tile(tb, v_stage(tb & 1), true, pg[0], ip[0]);
+      const DmaPlan k1 = plan_tile(tb + 1, k_stage((tb + 1) & 1), false, pg[1], ip[1]);
+#pragma unroll
+      for (int j = 0; j < kLoadsPerWave; ++j) {
+        issue_load(k0, j, false);
+        issue_load(v0, j, true);
+        issue_load(k1, j, false);
+      }
+    }
+    DmaPlan plan_v = plan_tile(tb + 1, v_stage((tb + 1) & 1), true, pg[1], ip[1]);
+    DmaPlan plan_k = plan_tile(tb + 2, k_stage(tb & 1), false, pg[2], ip[2]);
+    int page_a = pg[2], page_b = pg[3];  // pages of tiles kt+2, kt+3
+    int ip_a = ip[2], ip_b = ip[3];
     wait_lds_loads();
     __syncthreads();
     compute_s(tb & 1, sc);
+    mask_tile(sc, tb);
+    float mt;
+    {
+      float mx = 0.f;
+#pragma unroll
+      for (int st = 0; st < 15; ++st) mx = max_step(sc, mx, st);
+      mt = max_finish(sc, mx);
+    }
     for (int kt = tb; kt < t_end; ++kt) {
       wait_lds_loads();
       __syncthreads();
-      int pk = 0, pv = 0;
+      int page_c = 0;
       if constexpr (MODE == kPagedAligned) {
-        pk = __builtin_amdgcn_readfirstlane(page_k);
-        pv = page_prev;
-        page_prev = pk;
-        if (kt + 3 < t_end) page_k = fetch_page(kt + 3);
+        page_a = __builtin_amdgcn_readfirstlane(page_a);
+        page_b = __builtin_amdgcn_readfirstlane(page_b);
+        if (kt + 4 < t_end) page_c = fetch_page(kt + 4);
       }
-      const DmaPlan plan_v = plan_tile(kt + 1, v_stage((kt + 1) & 1), true, pv);
-      const DmaPlan plan_k = plan_tile(kt + 2, k_stage(kt & 1), false, pk);
-      const float moff = softmax_max(sc, kt);
-      mma_step(kt, sc, moff, plan_v, plan_k);
+      if constexpr (MODE == kPagedAny) {
+        plan_v = plan_tile(kt + 1, v_stage((kt + 1) & 1), true, 0, 0);
+        plan_k = plan_tile(kt + 2, k_stage(kt & 1), false, 0, 0);
+      }
+      const float moff = rescale(mt);
+      DmaPlan next_v = plan_v, next_k = plan_k;
+      mma_step(kt, sc, moff, plan_v, plan_k, page_a, ip_a, page_b, ip_b, next_v, next_k, mt);
+      plan_v = next_v;
+      plan_k = next_k;
+      page_a = page_b;
+      page_b = page_c;
+      ip_a = ip_b;
+      ip_b = next_in_page(ip_b);
     }
   }
 
@@ -586,7 +645,7 @@ __global__ __launch_bounds__(256, 2) void varlen_prefill_kernel(PrefillArgs a) {
 // Merges the split-K partial records of one (sequence, kv head, query tile):
 // thread t handles row t/2 and d range 64*(t%2) .. +63.
 template <int G, int MODE>
-__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(2 * kRows) void prefill_combine_kernel(PrefillArgs a) {
   constexpr int TQ = kRows / G;
   const int kvh = blockIdx.x, s = blockIdx.y, qt = blockIdx.z;
   const QTile qi = qtile_info<MODE>(a, s, qt, TQ);
@@ -635,12 +694,12 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillArgs a) {
 template <int G, int MODE>
 int launch_mode(const PrefillArgs& a, hipStream_t stream) {
   dim3 grid(a.num_kv_heads, a.batch, a.n_qtiles * a.n_splits);
-  hipLaunchKernelGGL((varlen_prefill_kernel<G, MODE>), grid, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((varlen_prefill_kernel<G, MODE>), grid, dim3(64 * kWaves), 0, stream, a);
   if (a.n_splits > 1) {
     const int st = nvk_launch_status();
     if (st != NVK_OK) return st;
     dim3 cgrid(a.num_kv_heads, a.batch, a.n_qtiles);
-    hipLaunchKernelGGL((prefill_combine_kernel<G, MODE>), cgrid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((prefill_combine_kernel<G, MODE>), cgrid, dim3(2 * kRows), 0, stream, a);
   }
   return nvk_launch_status();
 }
