@@ -6,10 +6,12 @@ Headline (`value`): paged GQA decode attention, Qwen3-0.6B shape: batch 64,
 (seeded).  A step is one decode-attention call over the batch (the split-K
 kernel and its combine pass).  `value` = algorithmic bytes of a step (unique
 K+V bytes of every context + q read + output written) / wall time per step,
-with every input resident in HBM.  Two more legs ride along in the same JSON
+with every input resident in HBM.  More legs ride along in the same JSON
 line: the KV-store scatter (4096 tokens into a 64-page cache, 5 % slots -1)
-in GB/s, the varlen prefill over a 512-token shared prefix (32 sequences,
-U{100..1024} new tokens) in TFLOP/s of unmasked QK^T + PV work, the
+in GB/s, the fused q/k RMSNorm + RoPE + KV-store prologue over one layer's
+4288 new tokens of the mixed step in GB/s (with the same steps as eager
+torch operations timed beside it), the varlen prefill over a 512-token
+shared prefix (32 sequences, U{100..1024} new tokens) in TFLOP/s of unmasked QK^T + PV work, the
 speculative-decode verification (32 sequences, 6 queries over U{1024..8192}
 keys, split-K) in GB/s, and a mixed step of 28 layers (per layer: KV-store of
 4288 tokens, 8 prefill chunks of 512 after U{0..1536} cached tokens, 192
@@ -26,7 +28,7 @@ achieved).  The CPU baseline is the numpy oracle on one host thread, timed on
 the same inputs.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                  [--legs decode,store,prefill,spec,mixed] [--eager]
+                  [--legs decode,store,prologue,prefill,spec,mixed] [--eager]
 
 --eager launches the steps one by one instead of replaying a graph (for
 counter collection with rocprofv3, which profiles individual dispatches).
@@ -59,7 +61,7 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--legs", default="decode,store,prefill,spec,mixed",
+    p.add_argument("--legs", default="decode,store,prologue,prefill,spec,mixed",
                    help="comma list of legs to run (decode, the headline, always runs)")
     p.add_argument("--eager", action="store_true",
                    help="launch steps one by one (no graph), e.g. under rocprofv3 --pmc")
@@ -195,6 +197,84 @@ def mixed_leg(torch, dev, args, orc, layers=28):
                           "frac": round(t_roof / ev, 4)})
 
 
+def prologue_leg(torch, dev, args, orc, bits):
+    """Fused q/k RMSNorm + RoPE + KV-store over the mixed step's 4288 new tokens
+    of one layer (4 rotated copies of qkv and of the 3300-page caches), and the
+    same steps as separate eager torch operations (the reference's
+    layernorm.py:16-26 / rotary_embedding.py:6-14 code, then the store) for
+    comparison."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from nanovllm_amd import qk_norm_rope_store, store_kvcache
+    from nanovllm_amd.workloads import prologue_case
+
+    log("building prologue workload (4288 tokens of the mixed step, 3300-page pool)")
+    pc = prologue_case()
+    hq, hkv, hd, eps = pc.hq, pc.hkv, pc.hd, pc.eps
+    copies = []
+    for _ in range(4):
+        c = pc.to(dev)
+        kc = torch.zeros(pc.pool_blocks, pc.block_size, hkv, hd, dtype=torch.bfloat16, device=dev)
+        copies.append((c, kc, torch.zeros_like(kc)))
+    fused = [(lambda c=c, kc=kc, vc=vc: qk_norm_rope_store(
+        c.positions, c.qkv, hq, hkv, hd, c.q_weight, c.k_weight, eps, c.cos_sin, kc, vc,
+        c.slot_mapping, return_k=False)) for c, kc, vc in copies]
+
+    def rms(x, w):                                        # layernorm.py:16-26, eager
+        dt = x.dtype
+        x = x.float()
+        var = x.pow(2).mean(dim=-1, keepdim=True)
+        x.mul_(torch.rsqrt(var + eps))
+        return x.to(dt).mul_(w)
+
+    def rope(x, cos, sin):                                # rotary_embedding.py:6-14, eager
+        x1, x2 = torch.chunk(x.float(), 2, dim=-1)
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+    def unfused_step(c, kc, vc):
+        q, k, v = c.qkv.split([hq * hd, hkv * hd, hkv * hd], dim=-1)
+        q, k, v = q.view(-1, hq, hd), k.view(-1, hkv, hd), v.view(-1, hkv, hd)
+        q, k = rms(q, c.q_weight), rms(k, c.k_weight)
+        cos, sin = c.cos_sin[c.positions].chunk(2, dim=-1)
+        q, k = rope(q, cos, sin), rope(k, cos, sin)
+        store_kvcache(k, v, kc, vc, c.slot_mapping)
+        return q
+
+    unfused = [(lambda c=c, kc=kc, vc=vc: unfused_step(c, kc, vc)) for c, kc, vc in copies]
+    n_valid = int((pc.slot_mapping >= 0).sum())
+    pbytes = orc.prologue_bytes(pc.n_tokens, n_valid, pc.n_unique_positions, hq, hkv, hd,
+                                write_k=False)
+    log("timing fused prologue")
+    wall, ev = time_graph(torch, fused, args.steps, args.warmup, args.eager)
+    log("timing the same steps as eager torch operations")
+    wall_u, _ = time_graph(torch, unfused, min(args.steps, 20), min(args.warmup, 3), args.eager)
+    leg = dict(ms_per_step=wall * 1e3, bytes_per_step=pbytes,
+               workload="q/k RMSNorm + RoPE + KV-store of one layer's 4288 new tokens "
+                        "(Qwen3-0.6B heads 16/8, head_dim 128; 8 prefill chunks of 512 + 192 "
+                        "decodes; 3300-page pool)",
+               unfused_torch_ms=round(wall_u * 1e3, 5),
+               roofline={"bound": "hbm", "achieved": round(pbytes / ev / 1e9, 2),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(pbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
+                         "traffic": traffic_for("prologue")})
+    if not args.no_cpu_baseline:
+        qkv_b, pos = bits(pc.qkv), pc.positions.numpy()
+        qw, kw, cs = bits(pc.q_weight), bits(pc.k_weight), pc.cos_sin.reshape(-1, hd).numpy()
+        sl = pc.slot_mapping.numpy()
+        kc_h = np.zeros((pc.pool_blocks, pc.block_size, hkv, hd), dtype=np.uint16)
+        vc_h = np.zeros_like(kc_h)
+        with threadpool_limits(1):
+            t = cpu_time(lambda: orc.qk_norm_rope_store(qkv_b, pos, qw, kw, eps, cs, hq, hkv, hd,
+                                                        kc_h, vc_h, sl), 5)
+        leg["cpu_baseline"] = {"value": round(pbytes / t / 1e9, 4), "unit": "GB/s", "cores": 1,
+                               "kind": "port",
+                               "sample": "the full 4288-token prologue through the numpy oracle "
+                                         "(norms, rotation, store), median of 5 reps on 1 host "
+                                         "thread"}
+    del copies, fused, unfused
+    return leg
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -288,6 +368,10 @@ def main():
         result["kv_store"] = leg
         del copies, st_fns
 
+    # ------------------------------------------------------------------ prologue
+    if "prologue" in legs:
+        result["prologue"] = prologue_leg(torch, dev, args, orc, bits)
+
     # ------------------------------------------------------------------ prefill
     if "prefill" in legs:
         log("building prefill workload (32 seqs, 512-token shared prefix)")
@@ -376,7 +460,7 @@ def main():
                      "traffic": traffic_for("decode")},
         "cpu_baseline": cpu,
     }
-    for k in ("kv_store", "prefill", "spec_verify", "mixed_step"):
+    for k in ("kv_store", "prologue", "prefill", "spec_verify", "mixed_step"):
         if k in result:
             line[k] = result[k]
     print(json.dumps(line), flush=True)

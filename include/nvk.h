@@ -190,6 +190,47 @@ size_t nvk_varlen_prefill_workspace_size(int32_t batch, int32_t max_seqlen_q,
                                          int32_t max_seqlen_k, int32_t num_q_heads,
                                          int32_t num_kv_heads, int32_t head_dim);
 
+/*
+ * Fused attention prologue: q/k RMSNorm + rotary embedding + KV-store.
+ * Replaces, per decoder layer, the steps between the qkv projection and the
+ * attention kernels: nanovllm/models/qwen3.py:79-86 (split, q_norm, k_norm,
+ * rotary_emb), i.e. RMSNorm.rms_forward (nanovllm/layers/layernorm.py:16-26),
+ * RotaryEmbedding.forward / apply_rotary_emb (rotary_embedding.py:6-14,
+ * 37-48), and the store_kvcache call of Attention.forward (attention.py:62-63).
+ *
+ * For every token t in [0, n_tokens) and head row of qkv[t] =
+ * [q (num_q_heads rows) | k (num_kv_heads rows) | v (num_kv_heads rows)],
+ * each row head_dim bf16 contiguous, token row stride qkv_row_stride:
+ *     q, k rows: x = float(row); x *= rsqrt(mean(x^2) + eps); x = bf16(x);
+ *                x = bf16(x * weight)            (q_norm_weight / k_norm_weight)
+ *                rotated by cos_sin_cache[positions[t]] (halves cos | sin,
+ *                rotate-half convention) and rounded to bf16
+ *     q_out[t, h]                      = rotated q row h
+ *     k_out[t, h]                      = rotated k row h        (k_out may be NULL)
+ *     k_cache row slot_mapping[t], h   = rotated k row h        (slot -1 skipped)
+ *     v_cache row slot_mapping[t], h   = v row h (bit copy)     (slot -1 skipped)
+ * Every f32 product and sum is rounded separately, as the reference's tensor
+ * operations are.  cos_sin_cache: float32 [max_position][row stride >=
+ * head_dim] (the reference's cos_sin_cache buffer, [max_position, 1,
+ * head_dim]); a position outside [0, max_position) is clamped into it (output
+ * unspecified, no out-of-bounds read).  slot_mapping NULL = no store (the
+ * reference skips the store while the caches are empty, attention.py:62);
+ * otherwise caches as in nvk_kv_store with cache_slots = num_blocks*block_size
+ * and slots outside [0, cache_slots) skipped.  positions: int64 [n_tokens].
+ * dtype: NVK_DTYPE_BF16.  head_dim: 128.  Pointers 16-byte aligned, strides
+ * multiples of 8 elements (cos_sin_row_stride of 4), n_tokens *
+ * (num_q_heads + 2*num_kv_heads) < 2^31.  One kernel, nothing allocated.
+ */
+int nvk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, int64_t n_tokens,
+                           const int64_t* positions, const void* q_norm_weight,
+                           const void* k_norm_weight, float eps, const float* cos_sin_cache,
+                           int64_t cos_sin_row_stride, int64_t max_position,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           void* q_out, int64_t q_out_stride_tok, int64_t q_out_stride_head,
+                           void* k_out, int64_t k_out_stride_tok, int64_t k_out_stride_head,
+                           void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                           int64_t cache_slots, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,217 @@
+// Fused attention prologue of a Qwen3 decoder layer for gfx950: per-head
+// RMSNorm of q and k, rotary embedding of q and k, and the KV-store scatter of
+// the rotated k and the raw v, in one pass over the packed qkv projection.
+//
+// Semantics (nanovllm/models/qwen3.py:79-86 then attention.py:62-63):
+//   q, k, v = qkv.split([Hq*D, Hkv*D, Hkv*D], -1), viewed [T, H, D]
+//   q = RMSNorm(q) ; k = RMSNorm(k)                  (layernorm.py:16-26)
+//       x.float(); x *= rsqrt(mean(x^2) + eps); x = bf16(x) * weight (bf16)
+//   q, k = rope(positions, q, k)                     (rotary_embedding.py:6-14, 37-48)
+//       x1, x2 = halves of x.float(); cos, sin = halves of cos_sin_cache[pos]
+//       y1 = x1*cos - x2*sin ; y2 = x2*cos + x1*sin ; bf16(cat(y1, y2))
+//   k_cache[slot] = k ; v_cache[slot] = v  for slot != -1  (attention.py:10-30)
+// Every f32 product and sum is rounded on its own (no fused multiply-add), as
+// the reference's separate tensor operations do.
+//
+// Data movement: the reference reads qkv, writes the normed q and k, reads
+// them back for the rotation, writes the rotated q and k, then the store reads
+// k and v again and writes the caches.  Here each head row (D = 128 bf16 =
+// 256 B) is read once and written once to each destination.
+//
+// Lane mapping: a row group of 16 lanes owns one head row of one token, 8
+// elements (16 B) per lane.  The row's sum of squares is a 16-lane DPP
+// reduction; the rotation partner of element i (i +- D/2) sits in lane
+// j ^ 8 of the same row group and is fetched with one DPP row rotation by 8.
+// A 256-thread workgroup covers 16 consecutive head rows of the flattened
+// [T][Hq + 2*Hkv] row space, so the reads of a workgroup are 4 KiB contiguous.
+#include "nvk_common.h"
+
+namespace {
+
+constexpr int kHD = 128;
+constexpr int kLanesPerRow = kHD / 8;  // 16
+constexpr int kRowsPerWG = 256 / kLanesPerRow;
+
+#define NVK_DPP_ROW_ROR8 0x128
+
+struct PrologueArgs {
+  const uint16_t* qkv;
+  int64_t qkv_row_stride;
+  int64_t n_tokens;
+  const int64_t* positions;
+  const uint16_t* q_weight;
+  const uint16_t* k_weight;
+  float eps;
+  const float* cos_sin;
+  int64_t cos_sin_stride;
+  int64_t max_position;
+  int num_q_heads, num_kv_heads;
+  uint16_t* q_out;
+  int64_t q_out_stride_tok, q_out_stride_head;
+  uint16_t* k_out;  // may be null
+  int64_t k_out_stride_tok, k_out_stride_head;
+  uint16_t* k_cache;  // null: no store
+  uint16_t* v_cache;
+  const int32_t* slot_mapping;
+  int64_t cache_slots;
+};
+
+__device__ __forceinline__ float bf16_round(float x) {
+  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) << 16);
+}
+
+__global__ __launch_bounds__(256) void qk_prologue_kernel(PrologueArgs a) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int j = lane & (kLanesPerRow - 1);
+  const int R = a.num_q_heads + 2 * a.num_kv_heads;
+  // rows of the flattened [T][R] space fit 31 bits (checked on the host)
+  const uint32_t row = blockIdx.x * kRowsPerWG + (threadIdx.x >> 4);
+  if ((int64_t)row >= a.n_tokens * R) return;  // whole row groups leave together
+  const int64_t t = row / (uint32_t)R;
+  const int r = (int)(row - (uint32_t)t * (uint32_t)R);
+
+  const nvk_u32x4 raw =
+      *reinterpret_cast<const nvk_u32x4*>(a.qkv + t * a.qkv_row_stride + (int64_t)r * kHD + 8 * j);
+  const bool is_q = r < a.num_q_heads;
+  const bool is_k = !is_q && r < a.num_q_heads + a.num_kv_heads;
+
+  int32_t slot = -1;
+  if (!is_q && a.slot_mapping != nullptr) {
+    slot = a.slot_mapping[t];
+    if ((int64_t)slot >= a.cache_slots) slot = -1;
+  }
+  const int64_t row_elems = (int64_t)a.num_kv_heads * kHD;
+
+  if (!is_q && !is_k) {  // v row: a plain copy into the cache
+    if (slot >= 0) {
+      const int kvh = r - a.num_q_heads - a.num_kv_heads;
+      *reinterpret_cast<nvk_u32x4*>(a.v_cache + (int64_t)slot * row_elems + kvh * kHD + 8 * j) = raw;
+    }
+    return;
+  }
+
+  float x[8];
+  const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = nvk_bf16lo_to_f32(w4[i]);
+    x[2 * i + 1] = nvk_bf16hi_to_f32(w4[i]);
+  }
+  // RMSNorm: var = mean(x^2) over the row (f32), x * rsqrt(var + eps) -> bf16,
+  // then times the bf16 weight -> bf16.
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+  ss = nvk_group_sum<kLanesPerRow>(ss);
+  const float rstd = rsqrtf(ss / (float)kHD + a.eps);
+  const nvk_u32x4 wraw =
+      *reinterpret_cast<const nvk_u32x4*>((is_q ? a.q_weight : a.k_weight) + 8 * j);
+  const uint32_t ww[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float n0 = bf16_round(x[2 * i] * rstd), n1 = bf16_round(x[2 * i + 1] * rstd);
+    x[2 * i] = bf16_round(n0 * nvk_bf16lo_to_f32(ww[i]));
+    x[2 * i + 1] = bf16_round(n1 * nvk_bf16hi_to_f32(ww[i]));
+  }
+  // Rotation: lanes 0-7 hold x1 (dims 0..63), lanes 8-15 x2 (dims 64..127);
+  // lane j's partner is lane j ^ 8 (a row rotation by 8 within 16 lanes).
+  int64_t pos = a.positions[t];
+  pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);
+  const float* cs = a.cos_sin + pos * a.cos_sin_stride + 8 * (j & 7);
+  const nvk_f32x4 c0 = *reinterpret_cast<const nvk_f32x4*>(cs);
+  const nvk_f32x4 c1 = *reinterpret_cast<const nvk_f32x4*>(cs + 4);
+  const nvk_f32x4 s0 = *reinterpret_cast<const nvk_f32x4*>(cs + kHD / 2);
+  const nvk_f32x4 s1 = *reinterpret_cast<const nvk_f32x4*>(cs + kHD / 2 + 4);
+  const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  const bool first_half = j < kLanesPerRow / 2;
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float other = nvk_dpp<NVK_DPP_ROW_ROR8>(x[e]);
+    const float a0 = x[e] * cv[e];
+    const float a1 = other * sv[e];
+    y[e] = first_half ? a0 - a1 : a0 + a1;  // x1*cos - x2*sin | x2*cos + x1*sin
+  }
+  nvk_u32x4 outw;
+  outw.x = nvk_pack_bf16x2(y[0], y[1]);
+  outw.y = nvk_pack_bf16x2(y[2], y[3]);
+  outw.z = nvk_pack_bf16x2(y[4], y[5]);
+  outw.w = nvk_pack_bf16x2(y[6], y[7]);
+  if (is_q) {
+    *reinterpret_cast<nvk_u32x4*>(a.q_out + t * a.q_out_stride_tok + (int64_t)r * a.q_out_stride_head +
+                                  8 * j) = outw;
+    return;
+  }
+  const int kvh = r - a.num_q_heads;
+  if (a.k_out != nullptr)
+    *reinterpret_cast<nvk_u32x4*>(a.k_out + t * a.k_out_stride_tok + (int64_t)kvh * a.k_out_stride_head +
+                                  8 * j) = outw;
+  if (slot >= 0)
+    *reinterpret_cast<nvk_u32x4*>(a.k_cache + (int64_t)slot * row_elems + kvh * kHD + 8 * j) = outw;
+}
+
+}  // namespace
+
+extern "C" int nvk_qk_norm_rope_store(
+    const void* qkv, int64_t qkv_row_stride, int64_t n_tokens, const int64_t* positions,
+    const void* q_norm_weight, const void* k_norm_weight, float eps, const float* cos_sin_cache,
+    int64_t cos_sin_row_stride, int64_t max_position, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, void* q_out, int64_t q_out_stride_tok, int64_t q_out_stride_head, void* k_out,
+    int64_t k_out_stride_tok, int64_t k_out_stride_head, void* k_cache, void* v_cache,
+    const int32_t* slot_mapping, int64_t cache_slots, int32_t dtype, void* stream) {
+  if (n_tokens < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || !(eps >= 0.f)) return NVK_EINVAL;
+  if (dtype != NVK_DTYPE_BF16 || head_dim != kHD) return NVK_EUNSUPPORTED;
+  if (n_tokens == 0) return NVK_OK;
+  if (!qkv || !positions || !q_norm_weight || !k_norm_weight || !cos_sin_cache || !q_out)
+    return NVK_EINVAL;
+  if (max_position <= 0 || cos_sin_row_stride < head_dim) return NVK_EINVAL;
+  const int64_t R = (int64_t)num_q_heads + 2 * num_kv_heads;
+  if (qkv_row_stride < R * head_dim) return NVK_EINVAL;
+  if (q_out_stride_head < head_dim || q_out_stride_tok < (int64_t)num_q_heads * q_out_stride_head)
+    return NVK_EINVAL;
+  if (k_out && (k_out_stride_head < head_dim ||
+                k_out_stride_tok < (int64_t)num_kv_heads * k_out_stride_head))
+    return NVK_EINVAL;
+  const bool store = slot_mapping != nullptr;
+  if (store && (!k_cache || !v_cache || cache_slots < 0)) return NVK_EINVAL;
+  // 16-byte vector access of every row and of the cos/sin rows.
+  if (((uintptr_t)qkv | (uintptr_t)q_out | (uintptr_t)k_out | (uintptr_t)q_norm_weight |
+       (uintptr_t)k_norm_weight | (uintptr_t)cos_sin_cache | (uintptr_t)k_cache |
+       (uintptr_t)v_cache) % 16)
+    return NVK_EALIGN;
+  if ((qkv_row_stride % 8) || (q_out_stride_tok % 8) || (q_out_stride_head % 8) ||
+      (k_out && ((k_out_stride_tok % 8) || (k_out_stride_head % 8))) || (cos_sin_row_stride % 4))
+    return NVK_EALIGN;
+  const int64_t rows = n_tokens * R;
+  if (rows > INT32_MAX) return NVK_EINVAL;
+  const int64_t grid = (rows + kRowsPerWG - 1) / kRowsPerWG;
+
+  PrologueArgs a;
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.qkv_row_stride = qkv_row_stride;
+  a.n_tokens = n_tokens;
+  a.positions = positions;
+  a.q_weight = static_cast<const uint16_t*>(q_norm_weight);
+  a.k_weight = static_cast<const uint16_t*>(k_norm_weight);
+  a.eps = eps;
+  a.cos_sin = cos_sin_cache;
+  a.cos_sin_stride = cos_sin_row_stride;
+  a.max_position = max_position;
+  a.num_q_heads = num_q_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.q_out = static_cast<uint16_t*>(q_out);
+  a.q_out_stride_tok = q_out_stride_tok;
+  a.q_out_stride_head = q_out_stride_head;
+  a.k_out = static_cast<uint16_t*>(k_out);
+  a.k_out_stride_tok = k_out_stride_tok;
+  a.k_out_stride_head = k_out_stride_head;
+  a.k_cache = store ? static_cast<uint16_t*>(k_cache) : nullptr;
+  a.v_cache = store ? static_cast<uint16_t*>(v_cache) : nullptr;
+  a.slot_mapping = store ? slot_mapping : nullptr;
+  a.cache_slots = cache_slots;
+  hipLaunchKernelGGL(qk_prologue_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
+  return nvk_launch_status();
+}

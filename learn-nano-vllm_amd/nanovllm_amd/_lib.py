@@ -45,6 +45,11 @@ SIGNATURES = {
                                           _c_ptr, ctypes.c_size_t, _c_i32, _c_ptr]),
     "nvk_varlen_prefill_workspace_size": (ctypes.c_size_t,
                                           [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "nvk_qk_norm_rope_store": (ctypes.c_int, [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr,
+                                              ctypes.c_float, _c_ptr, _c_i64, _c_i64, _c_i32,
+                                              _c_i32, _c_i32, _c_ptr, _c_i64, _c_i64, _c_ptr,
+                                              _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_i64,
+                                              _c_i32, _c_ptr]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -50,6 +50,9 @@ class Attention(nn.Module):
 
     forward(q [T,Hq,D], k [T,Hkv,D], v [T,Hkv,D]) reads the step metadata from
     get_context(); prefill returns [T,Hq,D], decode returns [B,1,Hq,D].
+    kv_stored=True (an addition; the reference has no such argument) skips the
+    store because the fused prologue (layers/prologue.py) already wrote the
+    caches; k may then be None unless the step is a dense prefill.
     """
 
     def __init__(self, num_heads, head_dim, scale, num_kv_heads):
@@ -60,10 +63,10 @@ class Attention(nn.Module):
         self.num_kv_heads = num_kv_heads
         self.k_cache = self.v_cache = torch.tensor([])
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_stored: bool = False):
         context = get_context()
         k_cache, v_cache = self.k_cache, self.v_cache
-        if k_cache.numel() and v_cache.numel():
+        if k_cache.numel() and v_cache.numel() and not kv_stored:
             store_kvcache(k, v, k_cache, v_cache, context.slot_mapping)
         if context.is_prefill:
             if context.block_tables is not None:    # prefix cache / later chunk

@@ -228,3 +228,27 @@ def mixed_layer_case(seed=3, n_chunks=8, chunk=512, cached_lo=0, cached_hi=1536,
                    v_cache=v_cache)
     meta.update(scale=hd ** -0.5)
     return Case(tensors, meta)
+
+
+def prologue_case(seed=5, hq=HQ, hkv=HKV, hd=HD, max_position=40960, rope_theta=1_000_000.0):
+    """The fused attention prologue over one layer of the mixed step: the 4288
+    new tokens (8 prefill chunks of 512 after U{0..1536} cached tokens + 192
+    decodes over U{256..4096}) with their positions and slots in a 3300-page
+    pool (the caches themselves are left to the caller: 1.7 GB each);
+    qkv ~ N(0, 2^2) bf16, norm weights ~ 1 + N(0, 0.2^2)."""
+    from nanovllm_amd.layers.prologue import rope_cos_sin_cache
+    tensors, meta = mixed_step_metadata()
+    gen = torch.Generator().manual_seed(seed)
+    chunk = meta["lens_q"][0]
+    pos = [p for lk in meta["lens_k"] for p in range(lk - chunk, lk)]
+    pos += [n - 1 for n in meta["dec_lens"]]
+    n = meta["n_tokens"]
+    assert len(pos) == n
+    qkv = (torch.randn(n, (hq + 2 * hkv) * hd, generator=gen) * 2.0).to(torch.bfloat16)
+    qw = (1.0 + 0.2 * torch.randn(hd, generator=gen)).to(torch.bfloat16)
+    kw = (1.0 + 0.2 * torch.randn(hd, generator=gen)).to(torch.bfloat16)
+    return Case(dict(qkv=qkv, positions=torch.tensor(pos, dtype=torch.int64), q_weight=qw,
+                     k_weight=kw, cos_sin=rope_cos_sin_cache(hd, max_position, rope_theta),
+                     slot_mapping=tensors["slot_mapping"]),
+                dict(n_tokens=n, hq=hq, hkv=hkv, hd=hd, eps=1e-6, pool_blocks=meta["pool_blocks"],
+                     block_size=meta["block_size"], n_unique_positions=len(set(pos))))

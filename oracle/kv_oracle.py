@@ -17,6 +17,12 @@ What it restates (numpy, bf16 carried as uint16 bit patterns):
                     query row i iff j <= i + Lk - Lq); rows that see no key are 0.
   slots_for         the slot formula slot = bt[p // bs] * bs + p % bs used by
                     model_runner.py:151-161, 181.
+  rms_norm          RMSNorm.rms_forward, nanovllm/layers/layernorm.py:16-26
+  apply_rotary_emb  rotary_embedding.py:6-14 (x.float(), halves, separately
+                    rounded f32 products, bf16 result)
+  qk_norm_rope_store  the prologue of Qwen3Attention.forward,
+                    nanovllm/models/qwen3.py:79-86, followed by the store of
+                    attention.py:62-63
 
 How each function is pinned (tests/test_oracle.py):
   kv_store          the guide's worked store example and test matrix
@@ -33,13 +39,26 @@ How each function is pinned (tests/test_oracle.py):
                     off-by-one limit) fails at least one of these checks.
   slots_for         the guide's known answer [14,15,0,3,20,21]
                     (master_nano-vllm-v2.md:2766-2776).
+  rms_norm          transformers' Qwen3RMSNorm (an independent library routine
+                    of the same definition) and closed forms: exact invariance
+                    under scaling the row by a power of two (eps = 0), unit
+                    mean square for unit weights, sign symmetry.
+  apply_rotary_emb  transformers' apply_rotary_pos_emb (rotate-half form) with
+                    its own Qwen3 cos/sin, bit for bit in float32; identity at
+                    position 0; the relative-position property
+                    <R(m)q, R(n)k> = <R(m+s)q, R(n+s)k>; pair norms preserved.
+                    A planted mistake (swapped halves, sign flip, interleaved
+                    pairs) fails these checks.
+  qk_norm_rope_store  composition of the two above plus kv_store, checked
+                    against a per-token loop of them.
 """
 from __future__ import annotations
 
 import numpy as np
 
 __all__ = ["bf16_to_f32", "f32_to_bf16", "kv_store", "slots_for", "gather_rows",
-           "paged_attention", "attention_bytes", "prefill_flops"]
+           "paged_attention", "attention_bytes", "prefill_flops", "rms_norm",
+           "apply_rotary_emb", "qk_norm_rope_store", "prologue_bytes"]
 
 
 # ---------------------------------------------------------------------------
@@ -166,6 +185,90 @@ def paged_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_seqlens_q, s
         out[q0:q1] = _attend(_as_f32(q[q0:q1]), _as_f32(ks), _as_f32(vs), scale, lk - lq,
                              _mutation)
     return out
+
+
+# ---------------------------------------------------------------------------
+# Attention prologue: q/k RMSNorm + RoPE (+ the KV store)
+# ---------------------------------------------------------------------------
+def rms_norm(x_bits: np.ndarray, weight_bits: np.ndarray, eps: float,
+             _mutation: str | None = None) -> np.ndarray:
+    """RMSNorm over the last dim, bf16 in / bf16 out (layernorm.py:16-26):
+    x = x.float(); x *= rsqrt(mean(x^2) + eps); x = bf16(x) * weight -> bf16.
+    rsqrt is evaluated in float64 and rounded once to float32."""
+    x = bf16_to_f32(x_bits)
+    var = np.mean(x * x, axis=-1, keepdims=True, dtype=np.float32)
+    if _mutation == "sum":
+        var = np.sum(x * x, axis=-1, keepdims=True, dtype=np.float32)
+    rstd = (1.0 / np.sqrt((var + np.float32(eps)).astype(np.float64))).astype(np.float32)
+    normed = f32_to_bf16(x * rstd)
+    w = bf16_to_f32(weight_bits)
+    return f32_to_bf16(bf16_to_f32(normed) * w)
+
+
+def apply_rotary_emb(x_bits: np.ndarray, cos: np.ndarray, sin: np.ndarray,
+                     _mutation: str | None = None) -> np.ndarray:
+    """rotary_embedding.py:6-14: x1, x2 = halves of x.float();
+    y1 = x1*cos - x2*sin, y2 = x2*cos + x1*sin (each product and sum rounded to
+    float32), cat -> bf16.  cos/sin broadcast against x's halves."""
+    x = bf16_to_f32(x_bits)
+    h = x.shape[-1] // 2
+    if _mutation == "interleaved":
+        x1, x2 = x[..., 0::2], x[..., 1::2]
+    else:
+        x1, x2 = x[..., :h], x[..., h:]
+    c = np.asarray(cos, dtype=np.float32)
+    s = np.asarray(sin, dtype=np.float32)
+    if _mutation == "sign":
+        s = -s
+    y1 = (x1 * c).astype(np.float32) - (x2 * s).astype(np.float32)
+    y2 = (x2 * c).astype(np.float32) + (x1 * s).astype(np.float32)
+    if _mutation == "swap":
+        y1, y2 = y2, y1
+    if _mutation == "interleaved":
+        y = np.empty_like(x)
+        y[..., 0::2], y[..., 1::2] = y1, y2
+        return f32_to_bf16(y)
+    return f32_to_bf16(np.concatenate([y1, y2], axis=-1))
+
+
+def qk_norm_rope_store(qkv_bits: np.ndarray, positions, q_weight_bits: np.ndarray,
+                       k_weight_bits: np.ndarray, eps: float, cos_sin: np.ndarray,
+                       num_q_heads: int, num_kv_heads: int, head_dim: int,
+                       k_cache: np.ndarray | None = None, v_cache: np.ndarray | None = None,
+                       slot_mapping=None):
+    """qwen3.py:79-86 + attention.py:62-63 on bf16 bit patterns.
+
+    qkv_bits [T, (Hq + 2*Hkv)*D]; cos_sin float32 [max_position, D] (cos | sin
+    halves).  Returns (q [T,Hq,D], k [T,Hkv,D], v [T,Hkv,D]) as uint16; with
+    caches and slot_mapping given, k and v are stored as kv_store does."""
+    t = qkv_bits.shape[0]
+    qs, ks = num_q_heads * head_dim, num_kv_heads * head_dim
+    q = qkv_bits[:, :qs].reshape(t, num_q_heads, head_dim)
+    k = qkv_bits[:, qs:qs + ks].reshape(t, num_kv_heads, head_dim)
+    v = np.ascontiguousarray(qkv_bits[:, qs + ks:qs + 2 * ks]).reshape(t, num_kv_heads, head_dim)
+    q = rms_norm(q, q_weight_bits, eps)
+    k = rms_norm(k, k_weight_bits, eps)
+    cs = np.asarray(cos_sin, dtype=np.float32)[np.asarray(positions, dtype=np.int64)]
+    cos, sin = cs[:, None, :head_dim // 2], cs[:, None, head_dim // 2:]
+    q = apply_rotary_emb(q, cos, sin)
+    k = apply_rotary_emb(k, cos, sin)
+    if k_cache is not None and slot_mapping is not None:
+        kv_store(k, v, k_cache, v_cache, slot_mapping)
+    return q, k, v
+
+
+def prologue_bytes(n_tokens: int, n_valid_slots: int, n_unique_positions: int,
+                   num_q_heads: int, num_kv_heads: int, head_dim: int, write_k: bool) -> int:
+    """HBM bytes the fused prologue must move: the qkv rows, positions and
+    slots read, one cos/sin row per distinct position, q written, k and v
+    rows written to the caches for valid slots (and k written out if asked)."""
+    row = head_dim * 2
+    rd = n_tokens * (num_q_heads + 2 * num_kv_heads) * row + n_tokens * (8 + 4)
+    rd += n_unique_positions * head_dim * 4
+    wr = n_tokens * num_q_heads * row + n_valid_slots * 2 * num_kv_heads * row
+    if write_k:
+        wr += n_tokens * num_kv_heads * row
+    return rd + wr
 
 
 # ---------------------------------------------------------------------------

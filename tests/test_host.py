@@ -79,6 +79,24 @@ def test_error_codes_without_launching():
     assert lib.nvk_varlen_prefill_workspace_size(32, 1024, 1536, 16, 8, 128) == 0
     # short key ranges are never split
     assert lib.nvk_varlen_prefill_workspace_size(1, 6, 512, 16, 8, 128) == 0
+    # fused prologue: (qkv, stride, T, pos, qw, kw, eps, cos_sin, cs_stride, max_pos, Hq, Hkv,
+    # D, q_out, strides, k_out, strides, k_cache, v_cache, slots, cache_slots, dtype, stream)
+    pro = [16, 32 * 128, 4, 16, 16, 16, 1e-6, 16, 128, 4096, 16, 8, 128, 16, 16 * 128, 128,
+           None, 0, 0, 16, 16, 16, 1 << 20, 0, None]
+    assert lib.nvk_qk_norm_rope_store(*pro[:12], 64, *pro[13:]) == -2     # head_dim 64
+    assert lib.nvk_qk_norm_rope_store(*pro[:23], 1, None) == -2           # fp16
+    zero = list(pro); zero[2] = 0
+    assert lib.nvk_qk_norm_rope_store(*zero) == 0                          # nothing to do
+    no_q = list(pro); no_q[13] = None
+    assert lib.nvk_qk_norm_rope_store(*no_q) == -1
+    narrow = list(pro); narrow[1] = 31 * 128                               # row < Hq+2Hkv heads
+    assert lib.nvk_qk_norm_rope_store(*narrow) == -1
+    mis = list(pro); mis[0] = 24                                           # qkv not 16-B aligned
+    assert lib.nvk_qk_norm_rope_store(*mis) == -3
+    no_cache = list(pro); no_cache[19] = None                              # slots without caches
+    assert lib.nvk_qk_norm_rope_store(*no_cache) == -1
+    huge = list(pro); huge[2] = 1 << 27                                    # > 2^31 head rows
+    assert lib.nvk_qk_norm_rope_store(*huge) == -1
 
 
 def test_cpu_tensors_are_rejected_not_served():
