@@ -15,6 +15,12 @@
  *                          block_table)
  *                          (nanovllm/layers/attention.py:64-70)
  *
+ * and one more fuses the steps just before them:
+ *
+ *   nvk_qk_norm_rope_store <- q_norm / k_norm / rotary_emb of Qwen3Attention.forward
+ *                          (nanovllm/models/qwen3.py:79-86) + the store of
+ *                          attention.py:62-63
+ *
  * Conventions shared by every entry point
  *   - All pointers are device pointers (hipMalloc / torch CUDA tensors) except
  *     where stated.  Strides are in ELEMENTS, not bytes.
@@ -218,8 +224,8 @@ size_t nvk_varlen_prefill_workspace_size(int32_t batch, int32_t max_seqlen_q,
  * otherwise caches as in nvk_kv_store with cache_slots = num_blocks*block_size
  * and slots outside [0, cache_slots) skipped.  positions: int64 [n_tokens].
  * dtype: NVK_DTYPE_BF16.  head_dim: 128.  Pointers 16-byte aligned, strides
- * multiples of 8 elements (cos_sin_row_stride of 4), n_tokens *
- * (num_q_heads + 2*num_kv_heads) < 2^31.  One kernel, nothing allocated.
+ * multiples of 8 elements (cos_sin_row_stride of 4), n_tokens < 2^31.  One
+ * kernel (one workgroup per token), nothing allocated.
  */
 int nvk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, int64_t n_tokens,
                            const int64_t* positions, const void* q_norm_weight,

@@ -95,7 +95,7 @@ def test_error_codes_without_launching():
     assert lib.nvk_qk_norm_rope_store(*mis) == -3
     no_cache = list(pro); no_cache[19] = None                              # slots without caches
     assert lib.nvk_qk_norm_rope_store(*no_cache) == -1
-    huge = list(pro); huge[2] = 1 << 27                                    # > 2^31 head rows
+    huge = list(pro); huge[2] = 1 << 31                                    # grid > 2^31 - 1
     assert lib.nvk_qk_norm_rope_store(*huge) == -1
 
 
