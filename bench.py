@@ -13,8 +13,10 @@ in GB/s, the fused q/k RMSNorm + RoPE + KV-store prologue over one layer's
 torch operations timed beside it), the varlen prefill over a 512-token
 shared prefix (32 sequences, U{100..1024} new tokens) in TFLOP/s of unmasked QK^T + PV work, the
 speculative-decode verification (32 sequences, 6 queries over U{1024..8192}
-keys, split-K) in GB/s, and a mixed step of 28 layers (per layer: KV-store of
-4288 tokens, 8 prefill chunks of 512 after U{0..1536} cached tokens, 192
+keys, split-K) in GB/s, the decode attention path of a 28-layer stack
+(fused prologue + paged decode per layer, B = 64) replayed from bucketed HIP
+graphs as the reference's run_model does, in GB/s, and a mixed step of 28
+layers (per layer: KV-store of 4288 tokens, 8 prefill chunks of 512 after U{0..1536} cached tokens, 192
 decodes over U{256..4096}; a separate KV pool per layer) as the fraction of
 its roofline time (decode and store bytes at HBM peak + prefill FLOPs at MFMA
 peak).
@@ -28,7 +30,7 @@ achieved).  The CPU baseline is the numpy oracle on one host thread, timed on
 the same inputs.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                  [--legs decode,store,prologue,prefill,spec,mixed] [--eager]
+                  [--legs decode,store,prologue,prefill,spec,graph,mixed] [--eager]
 
 --eager launches the steps one by one instead of replaying a graph (for
 counter collection with rocprofv3, which profiles individual dispatches).
@@ -59,9 +61,9 @@ def parse_args():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--legs", default="decode,store,prologue,prefill,spec,mixed",
+    p.add_argument("--legs", default="decode,store,prologue,prefill,spec,graph,mixed",
                    help="comma list of legs to run (decode, the headline, always runs)")
     p.add_argument("--eager", action="store_true",
                    help="launch steps one by one (no graph), e.g. under rocprofv3 --pmc")
@@ -275,6 +277,72 @@ def prologue_leg(torch, dev, args, orc, bits):
     return leg
 
 
+def decode_graph_leg(torch, dev, args, orc, layers=28):
+    """The decode attention path of a 28-layer Qwen3-0.6B stack, captured per
+    batch bucket and replayed as the reference's run_model does: per layer the
+    fused prologue (q/k norms, rotation, store of the new token) and the paged
+    decode over config 2's contexts (B = 64, U{100..2048}); every layer has
+    its own 1024-page cache (views of one [2, 28, 1024, 256, 8, 128]
+    allocation).  Timed as graph replays (run() with its host-side buffer
+    refresh) and as the same step launched eagerly."""
+    from nanovllm_amd.engine.graph_runner import DecodeGraphRunner
+    from nanovllm_amd.utils.context import reset_context, set_context
+    from nanovllm_amd.workloads import decode_case, decode_stack
+
+    dc = decode_case()
+    b, nb, w = 64, dc.k_cache.shape[0], dc.block_tables.shape[1]
+    log(f"building {layers}-layer decode stack (30 GB of KV cache) and capturing buckets")
+    stack, _, kv_cache, step = decode_stack(layers, nb, dev)
+    r = 16 + 2 * 8
+    runner = DecodeGraphRunner(step, b, w, inputs={"qkv": ((layers, r * 128), torch.bfloat16)},
+                               output=((layers, 16 * 128), torch.bfloat16), device=dev)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    qkv = (torch.randn(b, layers, r * 128, generator=gen, device=dev) * 2.0).to(torch.bfloat16)
+    lens = dc.context_lens.to(dev)
+    slots = torch.tensor([int(dc.block_tables[i, (n - 1) // 256]) * 256 + (n - 1) % 256
+                          for i, n in enumerate(dc.lens)], dtype=torch.int32, device=dev)
+    pos = (lens - 1).to(torch.int64)
+    steps, warm = min(args.steps, 20), min(args.warmup, 3)
+
+    def timed(n):
+        """(graph replay, eager) seconds per step for the first n sequences."""
+        set_context(False, slot_mapping=slots[:n], context_lens=lens[:n],
+                    block_tables=dc.block_tables[:n].to(dev))
+        try:
+            out = []
+            for fn in (lambda: runner.run(pos[:n], qkv=qkv[:n]), lambda: step(pos[:n], qkv[:n])):
+                for _ in range(warm):
+                    fn()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(steps):
+                    fn()
+                torch.cuda.synchronize()
+                out.append((time.perf_counter() - t0) / steps)
+            return out
+        finally:
+            reset_context()
+
+    log("timing graph replays and eager launches, B = 64 and B = 4")
+    t_graph, t_eager = timed(b)
+    t_graph4, t_eager4 = timed(4)
+    per_layer = (orc.attention_bytes(dc.lens, 8, 128, b, 16) +
+                 orc.prologue_bytes(b, b, b, 16, 8, 128, write_k=False))
+    total = layers * per_layer
+    del runner, stack, kv_cache
+    return dict(ms_per_step=round(t_graph * 1e3, 4), eager_ms_per_step=round(t_eager * 1e3, 4),
+                batch4={"ms_per_step": round(t_graph4 * 1e3, 4),
+                        "eager_ms_per_step": round(t_eager4 * 1e3, 4),
+                        "contexts": dc.lens[:4]},
+                layers=layers, bytes_per_step=total,
+                workload=f"{layers} layers x (fused q/k norm + RoPE + store of 64 new tokens, "
+                         "paged decode B=64 over U{100..2048}), bucket 64 of "
+                         "[1, 2, 4, 8, 16, 32, 48, 64], graph replays",
+                roofline={"bound": "hbm", "achieved": round(total / t_graph / 1e9, 2),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(total / t_graph / 1e9 / HBM_PEAK_GBS, 4)})
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -432,6 +500,10 @@ def main():
                       "traffic": traffic_for("spec_verify")})
         del copies, outs, sv_fns
 
+    # ------------------------------------------------------------------ decode graphs
+    if "graph" in legs:
+        result["decode_graph"] = decode_graph_leg(torch, dev, args, orc)
+
     # ------------------------------------------------------------------ mixed step
     if "mixed" in legs:
         result["mixed_step"] = mixed_leg(torch, dev, args, orc)
@@ -460,7 +532,7 @@ def main():
                      "traffic": traffic_for("decode")},
         "cpu_baseline": cpu,
     }
-    for k in ("kv_store", "prologue", "prefill", "spec_verify", "mixed_step"):
+    for k in ("kv_store", "prologue", "prefill", "spec_verify", "decode_graph", "mixed_step"):
         if k in result:
             line[k] = result[k]
     print(json.dumps(line), flush=True)

@@ -27,7 +27,7 @@
 // are ordered b-major, head block next, and the T chunks of the step are cut
 // into equal contiguous ranges, one per wave of a persistent grid of at most
 // 512 workgroups x 4 waves (static, so the launch can be captured in a graph;
-// when T is small only T/8 waves take part).  Every wave streams the same
+// when T is small only T/2 waves take part).  Every wave streams the same
 // number of bytes whatever the mix of context lengths.  Measured on MI355X, a
 // wave that issues one chunk, waits and computes it, with 8 waves per CU,
 // streams this access pattern at the rate of a plain read probe; deeper
@@ -50,7 +50,10 @@ constexpr int kLoads = 8;          // load instructions per tensor per chunk
 constexpr int kWavesPerWG = 4;
 constexpr int kMaxWGs = 512;       // 256 CUs x 2 workgroups (8 waves per CU)
 constexpr int kMaxBatch = 2048;    // sequences per call (LDS prefix table)
-constexpr int kMinChunks = 8;      // a wave streams at least this many chunks
+// A wave streams at least this many chunks.  Measured on MI355X: 2 against 8
+// takes a 4-sequence decode from 30 to 17 us and a 16-sequence one from 34 to
+// 27 us (more waves share a small step), and changes nothing from 64 up.
+constexpr int kMinChunks = 2;
 
 typedef __attribute__((address_space(4))) const int32_t nvk_const_i32;
 

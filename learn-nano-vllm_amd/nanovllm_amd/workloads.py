@@ -252,3 +252,55 @@ def prologue_case(seed=5, hq=HQ, hkv=HKV, hd=HD, max_position=40960, rope_theta=
                      slot_mapping=tensors["slot_mapping"]),
                 dict(n_tokens=n, hq=hq, hkv=hkv, hd=hd, eps=1e-6, pool_blocks=meta["pool_blocks"],
                      block_size=meta["block_size"], n_unique_positions=len(set(pos))))
+
+
+class _Norm:
+    """The two attributes of layernorm.RMSNorm the fused prologue reads."""
+
+    def __init__(self, weight, eps):
+        self.weight, self.eps = weight, eps
+
+
+class _Rope:
+    """The attribute of rotary_embedding.RotaryEmbedding the fused prologue reads."""
+
+    def __init__(self, cos_sin_cache):
+        self.cos_sin_cache = cos_sin_cache
+
+
+def decode_stack(num_layers, num_blocks, device, seed=6, hq=HQ, hkv=HKV, hd=HD,
+                 block_size=BLOCK, max_position=40960, rope_theta=1_000_000.0, eps=1e-6):
+    """The attention path of a Qwen3 decoder stack on one device: per layer an
+    Attention whose caches are views of one [2, L, NB, bs, Hkv, D] allocation
+    (allocate_kv_cache, model_runner.py:103-121; filled with N(0,1) bf16),
+    q/k norm weights ~ 1 + N(0, 0.2^2), one shared rotary cache.  Returns
+    (layers, rope, kv_cache, step): layers[i] = (attn, q_norm, k_norm) and
+    step(positions [bs], qkv [bs, L, (Hq+2Hkv)*D]) -> [bs, L, Hq*D] runs, per
+    layer, the fused prologue (norms, rotation, store) and the attention of
+    the current Context."""
+    from nanovllm_amd.layers.attention import Attention
+    from nanovllm_amd.layers.prologue import attention_with_prologue, rope_cos_sin_cache
+    gen = torch.Generator(device=device).manual_seed(seed)
+    kv_cache = torch.empty(2, num_layers, num_blocks, block_size, hkv, hd, dtype=torch.bfloat16,
+                           device=device)
+    for i in range(num_layers):
+        for j in range(2):
+            for b in range(0, num_blocks, 256):
+                n = min(256, num_blocks - b)
+                kv_cache[j, i, b:b + n].copy_(torch.randn(n, block_size, hkv, hd, generator=gen,
+                                                          device=device))
+    rope = _Rope(rope_cos_sin_cache(hd, max_position, rope_theta, device=device))
+    layers = []
+    for i in range(num_layers):
+        attn = Attention(hq, hd, hd ** -0.5, hkv)
+        attn.k_cache, attn.v_cache = kv_cache[0, i], kv_cache[1, i]
+        w = lambda: (1.0 + 0.2 * torch.randn(hd, generator=gen, device=device)).to(torch.bfloat16)
+        layers.append((attn, _Norm(w(), eps), _Norm(w(), eps)))
+
+    def step(positions, qkv):
+        outs = [attention_with_prologue(attn, positions, qkv[:, i], qn, kn, rope)
+                .reshape(positions.numel(), hq * hd)
+                for i, (attn, qn, kn) in enumerate(layers)]
+        return torch.stack(outs, dim=1)
+
+    return layers, rope, kv_cache, step

@@ -1,0 +1,88 @@
+"""Bucketed HIP-graph decode of a multi-layer attention stack, replayed the way
+the reference's run_model does (model_runner.py:195-257): graphs captured per
+bucket with all-zero metadata, live batches smaller than their bucket, padded
+rows with slot -1 and context 0, stale block-table tails from earlier
+replays.  Every layer runs the fused prologue (norms, rotation, store) and the
+paged decode; the result is checked against the oracle per layer."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as orc
+from nanovllm_amd.engine.graph_runner import DecodeGraphRunner, graph_buckets
+from nanovllm_amd.utils.context import reset_context, set_context
+from nanovllm_amd.workloads import decode_stack
+from tests.gpu_utils import (assert_attn_close, assert_rotated_close, bits, from_bits,
+                             oracle_decode, say)
+
+L, NB, BS, W, MAX_BS = 2, 128, 256, 8, 32
+HQ, HKV, D = 16, 8, 128
+
+
+def test_graph_buckets_follow_the_reference():
+    assert graph_buckets(512)[:6] == [1, 2, 4, 8, 16, 32] and graph_buckets(512)[-1] == 512
+    assert graph_buckets(8) == [1, 2, 4, 8]
+
+
+@pytest.mark.gpu
+def test_bucketed_decode_graph_replays_match_oracle():
+    say("decode graph: capture buckets")
+    dev = torch.device("cuda:0")
+    layers, rope, kv_cache, step = decode_stack(L, NB, dev, seed=31)
+    runner = DecodeGraphRunner(step, MAX_BS, W, inputs={"qkv": ((L, (HQ + 2 * HKV) * D),
+                                                                torch.bfloat16)},
+                               output=((L, HQ * D), torch.bfloat16), device=dev)
+    assert runner.buckets == [1, 2, 4, 8, 16, 32]
+    cos_sin = rope.cos_sin_cache.reshape(-1, D).cpu().numpy()
+    gen = torch.Generator().manual_seed(32)
+    for rep, live in enumerate([5, 16, 20, 1, 32]):
+        perm = torch.randperm(NB, generator=gen).tolist()
+        lens = torch.randint(1, 1500, (live,), generator=gen, dtype=torch.int32)
+        tables, nxt = [], 0
+        for n in lens.tolist():
+            need = (n + BS - 1) // BS
+            tables.append(perm[nxt:nxt + need])
+            nxt += need
+        assert nxt <= NB
+        w = max(len(t) for t in tables)
+        bt = torch.full((live, w), -1, dtype=torch.int32)
+        for i, t in enumerate(tables):
+            bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+        slots = torch.tensor([t[(n - 1) // BS] * BS + (n - 1) % BS for t, n in zip(tables, lens.tolist())],
+                             dtype=torch.int32)
+        pos = (lens - 1).to(torch.int64)
+        qkv = (torch.randn(live, L, (HQ + 2 * HKV) * D, generator=gen) * 2.0).to(torch.bfloat16)
+        before = bits(kv_cache).copy()
+        say(f"decode graph replay {rep}: live={live} bucket={runner.bucket(live)}")
+        set_context(False, slot_mapping=slots.to(dev), context_lens=lens.to(dev),
+                    block_tables=bt.to(dev))
+        try:
+            out = runner.run(pos.to(dev), qkv=qkv.to(dev)).clone()
+            padded = runner.outputs[live:runner.bucket(live)].clone()
+            torch.cuda.synchronize()
+        finally:
+            reset_context()
+        assert out.shape == (live, L, HQ * D)
+        assert padded.eq(0).all(), "padded rows must be zero"
+        after = bits(kv_cache)
+        sl = slots.numpy().astype(np.int64)
+        for i, (attn, qn, kn) in enumerate(layers):
+            kc_ref, vc_ref = before[0, i].copy(), before[1, i].copy()
+            q_ref, k_ref, _ = orc.qk_norm_rope_store(
+                bits(qkv[:, i]), pos.numpy(), bits(qn.weight), bits(kn.weight), qn.eps, cos_sin,
+                HQ, HKV, D, kc_ref, vc_ref, sl)
+            # v rows bit-exact, every other cache row untouched
+            assert np.array_equal(after[1, i], vc_ref), f"layer {i}: v cache"
+            kc_got = after[0, i].reshape(NB * BS, HKV, D)
+            untouched = np.ones(NB * BS, dtype=bool)
+            untouched[sl] = False
+            assert np.array_equal(kc_got[untouched],
+                                  before[0, i].reshape(NB * BS, HKV, D)[untouched])
+            assert_rotated_close(kc_got[sl], k_ref, f"layer {i}: cached k")
+            ref = oracle_decode(from_bits(q_ref, "cpu"), from_bits(after[0, i], "cpu"),
+                                from_bits(after[1, i], "cpu"), bt, lens, BS, D ** -0.5)
+            assert_attn_close(out[:, i].reshape(live, HQ, D), ref, f"replay {rep} layer {i}")
+    with pytest.raises(ValueError):
+        runner.run(torch.zeros(MAX_BS + 1, dtype=torch.int64, device=dev),
+                   qkv=torch.zeros(MAX_BS + 1, L, (HQ + 2 * HKV) * D, dtype=torch.bfloat16,
+                                   device=dev))

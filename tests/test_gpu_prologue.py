@@ -19,7 +19,8 @@ from oracle import kv_oracle as orc
 from nanovllm_amd import attention_with_prologue, qk_norm_rope_store, rope_cos_sin_cache
 from nanovllm_amd.layers.attention import Attention
 from nanovllm_amd.utils.context import reset_context, set_context
-from tests.gpu_utils import assert_attn_close, bits, from_bits, oracle_decode, say
+from tests.gpu_utils import (assert_attn_close, assert_rotated_close, bits, from_bits,
+                             oracle_decode, say)
 
 pytestmark = pytest.mark.gpu
 
@@ -54,18 +55,6 @@ def _case(t, hq, hkv, nb, bs, seed, row_pad=0):
     return qkv_full, qkv, qw, kw, pos, kc, vc, perm
 
 
-def _check_rotated(got_bits, ref_bits, what):
-    got = orc.bf16_to_f32(got_bits).astype(np.float64)
-    ref = orc.bf16_to_f32(ref_bits).astype(np.float64)
-    same = got_bits == ref_bits
-    assert same.mean() > 0.999, f"{what}: {(~same).sum()} of {same.size} differ"
-    h = D // 2
-    scale = np.abs(ref[..., :h]) + np.abs(ref[..., h:])
-    scale = np.concatenate([scale, scale], axis=-1)
-    bad = np.abs(got - ref) > 2.0 ** -6 * scale + 1e-30
-    assert not bad.any(), f"{what}: {bad.sum()} elements beyond 2 bf16 ulps"
-
-
 def _oracle(qkv, qw, kw, pos, kc, vc, slots, cos_sin, hq, hkv):
     kc_ref, vc_ref = bits(kc).copy(), bits(vc).copy()
     sl = slots.numpy().astype(np.int64)
@@ -88,8 +77,8 @@ def test_prologue_matches_oracle(cos_sin, t, hq, hkv):
     q, k, v = qk_norm_rope_store(pos.to(dev), qkv.to(dev), hq, hkv, D, qw.to(dev), kw.to(dev),
                                  EPS, cos_sin.to(dev), kc_d, vc_d, slots.to(dev))
     torch.cuda.synchronize()
-    _check_rotated(bits(q), q_ref, "q")
-    _check_rotated(bits(k), k_ref, "k")
+    assert_rotated_close(bits(q), q_ref, "q")
+    assert_rotated_close(bits(k), k_ref, "k")
     assert np.array_equal(bits(v), v_ref)
     # caches: v rows bit-exact, k rows equal to the returned k, the rest untouched
     sl = slots.numpy().astype(np.int64)
@@ -116,7 +105,7 @@ def test_prologue_padded_rows_no_store_no_k(cos_sin):
                                  cos_sin.to(dev), return_k=False)
     torch.cuda.synchronize()
     assert k is None
-    _check_rotated(bits(q), q_ref, "q")
+    assert_rotated_close(bits(q), q_ref, "q")
     assert torch.equal(kc_d.cpu(), kc) and torch.equal(vc_d.cpu(), vc)
 
 
