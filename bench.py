@@ -15,8 +15,9 @@ shared prefix (32 sequences, U{100..1024} new tokens) in TFLOP/s of unmasked QK^
 speculative-decode verification (32 sequences, 6 queries over U{1024..8192}
 keys, split-K) in GB/s, the decode attention path of a 28-layer stack
 (fused prologue + paged decode per layer, B = 64) replayed from bucketed HIP
-graphs as the reference's run_model does, in GB/s, and a mixed step of 28
-layers (per layer: KV-store of 4288 tokens, 8 prefill chunks of 512 after U{0..1536} cached tokens, 192
+graphs as the reference's run_model does, in GB/s, the step metadata built
+by the reference's host loops against the device builders (ms per call), and
+a mixed step of 28 layers (per layer: KV-store of 4288 tokens, 8 prefill chunks of 512 after U{0..1536} cached tokens, 192
 decodes over U{256..4096}; a separate KV pool per layer) as the fraction of
 its roofline time (decode and store bytes at HBM peak + prefill FLOPs at MFMA
 peak).
@@ -30,7 +31,8 @@ achieved).  The CPU baseline is the numpy oracle on one host thread, timed on
 the same inputs.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                  [--legs decode,store,prologue,prefill,spec,graph,mixed] [--eager]
+                  [--legs decode,store,prologue,prefill,spec,graph,metadata,mixed]
+                  [--eager]
 
 --eager launches the steps one by one instead of replaying a graph (for
 counter collection with rocprofv3, which profiles individual dispatches).
@@ -63,7 +65,7 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--legs", default="decode,store,prologue,prefill,spec,graph,mixed",
+    p.add_argument("--legs", default="decode,store,prologue,prefill,spec,graph,metadata,mixed",
                    help="comma list of legs to run (decode, the headline, always runs)")
     p.add_argument("--eager", action="store_true",
                    help="launch steps one by one (no graph), e.g. under rocprofv3 --pmc")
@@ -343,6 +345,69 @@ def decode_graph_leg(torch, dev, args, orc, layers=28):
                           "frac": round(total / t_graph / 1e9 / HBM_PEAK_GBS, 4)})
 
 
+def metadata_leg(torch, dev, args):
+    """Step metadata built by the reference's host loops (restated in
+    engine/metadata.py) against the device builders, wall time per call
+    including the upload and a device synchronisation: a chunked-prefill step
+    of 64 sequences (U{0..1536} cached + U{100..1024} new tokens) and a
+    512-sequence decode step over U{256..4096}."""
+    import random
+    from nanovllm_amd.engine import metadata
+    from nanovllm_amd.engine.device_metadata import prepare_decode_device, prepare_prefill_device
+    from nanovllm_amd.engine.sequence import Sequence
+    from nanovllm_amd.utils.context import reset_context
+
+    rng = random.Random(8)
+    bs = 256
+    pages = list(range(64 * 11 + 512 * 17))
+    rng.shuffle(pages)
+    nxt = 0
+    pf = []
+    for _ in range(64):
+        c, m = rng.randint(0, 1536), rng.randint(100, 1024)
+        need = (c + m + bs - 1) // bs
+        pf.append(Sequence([rng.randint(0, 150000) for _ in range(c + m)],
+                           block_table=pages[nxt:nxt + need], num_cached_tokens=c,
+                           num_scheduled_tokens=m))
+        nxt += need
+    dc = []
+    for _ in range(512):
+        n = rng.randint(256, 4096)
+        need = (n + bs - 1) // bs
+        dc.append(Sequence([rng.randint(0, 150000) for _ in range(n)],
+                           block_table=pages[nxt:nxt + need]))
+        nxt += need
+
+    def wall(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+            reset_context()
+        return statistics.median(ts)
+
+    log("timing step metadata builders (host loops vs device kernel)")
+    reps = 20
+    res = {
+        "prefill_64_seqs": {
+            "tokens": sum(q.num_scheduled_tokens for q in pf),
+            "host_loops_ms": round(wall(lambda: metadata.prepare_prefill(pf, bs, dev), reps) * 1e3, 3),
+            "device_ms": round(wall(lambda: prepare_prefill_device(pf, bs, dev), reps) * 1e3, 3)},
+        "decode_512_seqs": {
+            "host_loops_ms": round(wall(lambda: metadata.prepare_decode(dc, bs, dev), reps) * 1e3, 3),
+            "device_ms": round(wall(lambda: prepare_decode_device(dc, bs, dev), reps) * 1e3, 3)},
+    }
+    res["workload"] = ("slot_mapping / positions / cu_seqlens / padded block tables of a "
+                       "64-sequence chunked prefill and a 512-sequence decode, median of "
+                       f"{reps} calls, wall time with the device synchronised")
+    return res
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -504,6 +569,10 @@ def main():
     if "graph" in legs:
         result["decode_graph"] = decode_graph_leg(torch, dev, args, orc)
 
+    # ------------------------------------------------------------------ step metadata
+    if "metadata" in legs:
+        result["step_metadata"] = metadata_leg(torch, dev, args)
+
     # ------------------------------------------------------------------ mixed step
     if "mixed" in legs:
         result["mixed_step"] = mixed_leg(torch, dev, args, orc)
@@ -532,7 +601,8 @@ def main():
                      "traffic": traffic_for("decode")},
         "cpu_baseline": cpu,
     }
-    for k in ("kv_store", "prologue", "prefill", "spec_verify", "decode_graph", "mixed_step"):
+    for k in ("kv_store", "prologue", "prefill", "spec_verify", "decode_graph", "step_metadata",
+              "mixed_step"):
         if k in result:
             line[k] = result[k]
     print(json.dumps(line), flush=True)

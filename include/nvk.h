@@ -237,6 +237,47 @@ int nvk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, int64_t n_to
                            void* k_cache, void* v_cache, const int32_t* slot_mapping,
                            int64_t cache_slots, int32_t dtype, void* stream);
 
+/*
+ * Device-side step metadata.
+ * Replaces the per-token host loops of ModelRunner.prepare_prefill /
+ * prepare_decode / prepare_block_tables (nanovllm/engine/model_runner.py:
+ * 123-188) and the graph-buffer refresh of run_model (model_runner.py:
+ * 204-210).  Block tables come compressed: row b is
+ * bt_ids[bt_offsets[b] .. bt_offsets[b+1]) (int32 [batch+1] offsets).
+ *
+ * nvk_prefill_metadata: per sequence b, num_cached[b] cached and num_new[b]
+ * new (scheduled) tokens; n_tokens = sum(num_new).  Writes
+ *   cu_seqlens_q [batch+1] = exclusive prefix of num_new,
+ *   cu_seqlens_k [batch+1] = exclusive prefix of num_cached + num_new,
+ *   positions    [n_tokens] int64: num_cached[b] .. num_cached[b]+num_new[b]-1,
+ *   slot_mapping [n_tokens]: block_table[p / block_size] * block_size + p % block_size
+ *                (-1 for a sequence without pages, or past its table),
+ *   block_tables [batch][table_width], -1 padded (NULL = not written; the
+ *                reference builds it only when some sequence has cached tokens).
+ * batch <= 8192.  bt_ids may be NULL when no sequence has pages.
+ *
+ * nvk_decode_metadata: per sequence b of length seq_lens[b] (counting the new
+ * token), rows b < batch: context_lens = len, positions = len - 1,
+ *   slot = block_table[-1] * block_size + (len - 1) % block_size (the
+ *   reference's block_table[-1]*bs + last_block_num_tokens - 1), and
+ *   block_tables row b = its pages, -1 padded to table_width (row stride
+ *   table_row_stride; columns >= table_width untouched);
+ * rows batch <= b < padded_batch (graph padding): slot -1, context 0;
+ *   positions and table rows there are untouched.
+ * Both: one kernel, nothing allocated, asynchronous on `stream`.
+ */
+int nvk_prefill_metadata(const int32_t* num_cached, const int32_t* num_new,
+                         const int32_t* bt_offsets, const int32_t* bt_ids, int32_t batch,
+                         int32_t block_size, int32_t table_width, int64_t n_tokens,
+                         int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, int64_t* positions,
+                         int32_t* slot_mapping, int32_t* block_tables, void* stream);
+
+int nvk_decode_metadata(const int32_t* seq_lens, const int32_t* bt_offsets,
+                        const int32_t* bt_ids, int32_t batch, int32_t padded_batch,
+                        int32_t block_size, int32_t table_width, int64_t table_row_stride,
+                        int32_t* context_lens, int64_t* positions, int32_t* slot_mapping,
+                        int32_t* block_tables, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,11 @@ SIGNATURES = {
                                               _c_i32, _c_i32, _c_ptr, _c_i64, _c_i64, _c_ptr,
                                               _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_i64,
                                               _c_i32, _c_ptr]),
+    "nvk_prefill_metadata": (ctypes.c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i32, _c_i32, _c_i32,
+                                            _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                            _c_ptr]),
+    "nvk_decode_metadata": (ctypes.c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i32, _c_i32, _c_i32, _c_i32,
+                                           _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -77,6 +77,18 @@ class DecodeGraphRunner:
     def bucket(self, bs: int) -> int:
         return next(x for x in self.buckets if x >= bs)
 
+    def replay(self, bs: int, **inputs: torch.Tensor) -> torch.Tensor:
+        """Replay the bucket of a live batch of bs whose metadata and positions
+        are already in the static buffers (written by
+        device_metadata.prepare_decode_device(..., into=self)); ``inputs``
+        are copied into the live rows first.  Returns outputs[:bs]."""
+        if bs > self.max_bs:
+            raise ValueError(f"batch {bs} above the largest captured bucket {self.max_bs}")
+        for name, value in inputs.items():
+            self.inputs[name][:bs] = value
+        self.graphs[self.bucket(bs)].replay()
+        return self.outputs[:bs]
+
     def run(self, positions: torch.Tensor, **inputs: torch.Tensor) -> torch.Tensor:
         """Replay for the live batch; metadata from get_context() (prepare_decode),
         as run_model does (model_runner.py:200-211).  Returns outputs[:bs] (a

@@ -97,6 +97,20 @@ def test_error_codes_without_launching():
     assert lib.nvk_qk_norm_rope_store(*no_cache) == -1
     huge = list(pro); huge[2] = 1 << 31                                    # grid > 2^31 - 1
     assert lib.nvk_qk_norm_rope_store(*huge) == -1
+    # step metadata: (cached, new, offsets, ids, B, bs, width, T, cu_q, cu_k, pos, slots, tables)
+    assert lib.nvk_prefill_metadata(16, 16, 16, 16, 9000, 256, 4, 10, 16, 16, 16, 16, 16,
+                                    None) == -2                            # batch > 8192
+    assert lib.nvk_prefill_metadata(None, None, None, None, 0, 256, 0, 0, None, None, None, None,
+                                    None, None) == 0                       # empty step
+    assert lib.nvk_prefill_metadata(16, 16, 16, 16, 4, 0, 4, 10, 16, 16, 16, 16, 16,
+                                    None) == -1                            # block size 0
+    assert lib.nvk_prefill_metadata(16, 16, 16, 16, 4, 256, 4, 10, 16, 16, None, 16, 16,
+                                    None) == -1                            # no positions
+    # (lens, offsets, ids, B, padded, bs, width, stride, ctx, pos, slots, tables)
+    assert lib.nvk_decode_metadata(16, 16, 16, 8, 4, 256, 4, 4, 16, 16, 16, 16, None) == -1
+    assert lib.nvk_decode_metadata(16, 16, 16, 4, 8, 256, 4, 2, 16, 16, 16, 16, None) == -1
+    assert lib.nvk_decode_metadata(None, None, None, 0, 0, 256, 0, 0, None, None, None, None,
+                                   None) == 0
 
 
 def test_cpu_tensors_are_rejected_not_served():
@@ -187,3 +201,10 @@ def test_graph_buffers_pad_rows_like_run_model():
     assert g.context_lens.tolist() == [6, 10] + [0] * 6
     assert g.block_tables[:2].tolist() == [[1, -1, 77, 77], [2, 3, 77, 77]]
     assert g.block_tables[2:].eq(77).all()
+
+
+def test_pack_block_tables_is_the_compressed_table():
+    from nanovllm_amd.engine.device_metadata import pack_block_tables
+    seqs = [Sequence([1, 2, 3], block_table=[4, 5]), Sequence([1], block_table=[]),
+            Sequence([1] * 9, block_table=[7, 8, 9])]
+    assert pack_block_tables(seqs) == ([0, 2, 2, 5], [4, 5, 7, 8, 9], 3)
