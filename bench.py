@@ -16,7 +16,8 @@ speculative-decode verification (32 sequences, 6 queries over U{1024..8192}
 keys, split-K) in GB/s, the decode attention path of a 28-layer stack
 (fused prologue + paged decode per layer, B = 64) replayed from bucketed HIP
 graphs as the reference's run_model does, in GB/s, the step metadata built
-by the reference's host loops against the device builders (ms per call), and
+by the reference's host loops against the device builders (ms per call), the
+sampler over Qwen3-sized logits against the reference's torch operations, and
 a mixed step of 28 layers (per layer: KV-store of 4288 tokens, 8 prefill chunks of 512 after U{0..1536} cached tokens, 192
 decodes over U{256..4096}; a separate KV pool per layer) as the fraction of
 its roofline time (decode and store bytes at HBM peak + prefill FLOPs at MFMA
@@ -31,7 +32,7 @@ achieved).  The CPU baseline is the numpy oracle on one host thread, timed on
 the same inputs.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                  [--legs decode,store,prologue,prefill,spec,graph,metadata,mixed]
+                  [--legs decode,store,prologue,prefill,spec,graph,metadata,sampler,mixed]
                   [--eager]
 
 --eager launches the steps one by one instead of replaying a graph (for
@@ -65,7 +66,8 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--legs", default="decode,store,prologue,prefill,spec,graph,metadata,mixed",
+    p.add_argument("--legs",
+                   default="decode,store,prologue,prefill,spec,graph,metadata,sampler,mixed",
                    help="comma list of legs to run (decode, the headline, always runs)")
     p.add_argument("--eager", action="store_true",
                    help="launch steps one by one (no graph), e.g. under rocprofv3 --pmc")
@@ -408,6 +410,45 @@ def metadata_leg(torch, dev, args):
     return res
 
 
+def sampler_leg(torch, dev, args):
+    """Temperature sampling of the next tokens from Qwen3-0.6B-sized logits
+    (vocab 151936, bf16) for 64 and 512 sequences: the fused kernel (one read
+    of the logits, Philox noise) against the reference's torch operations
+    (sampler.py:7-12 without torch.compile: float, div, softmax, exponential_,
+    clamp_min_, div_, argmax), each timed as a 20-call HIP graph."""
+    from nanovllm_amd.layers.sampler import Sampler
+
+    vocab = 151936
+    out = {}
+    sampler = Sampler()
+
+    def torch_sampler(logits, temps):
+        x = logits.float().div_(temps.unsqueeze(dim=1))
+        probs = torch.softmax(x, dim=-1)
+        return probs.div_(torch.empty_like(probs).exponential_(1).clamp_min_(1e-10)).argmax(dim=-1)
+
+    for b in (64, 512):
+        gen = torch.Generator(device=dev).manual_seed(b)
+        logits = [(torch.randn(b, vocab, generator=gen, device=dev) * 3).to(torch.bfloat16)
+                  for _ in range(4)]
+        temps = torch.full((b,), 0.8, device=dev)
+        nbytes = b * vocab * 2 + b * 8
+        fused = [(lambda x=x: sampler(x, temps)) for x in logits]
+        ref = [(lambda x=x: torch_sampler(x, temps)) for x in logits]
+        log(f"timing sampler B={b}")
+        _, ev = time_graph(torch, fused, 20, 3, args.eager)
+        _, ev_ref = time_graph(torch, ref, 20, 3, args.eager)
+        out[f"batch_{b}"] = {"ms_per_call": round(ev * 1e3, 4),
+                             "torch_ops_ms_per_call": round(ev_ref * 1e3, 4),
+                             "bytes_per_call": nbytes,
+                             "roofline": {"bound": "hbm", "achieved": round(nbytes / ev / 1e9, 2),
+                                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                          "frac": round(nbytes / ev / 1e9 / HBM_PEAK_GBS, 4)}}
+        del logits, fused, ref
+    out["workload"] = "next-token sampling over bf16 logits [B, 151936], temperature 0.8"
+    return out
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -573,6 +614,10 @@ def main():
     if "metadata" in legs:
         result["step_metadata"] = metadata_leg(torch, dev, args)
 
+    # ------------------------------------------------------------------ sampler
+    if "sampler" in legs:
+        result["sampler"] = sampler_leg(torch, dev, args)
+
     # ------------------------------------------------------------------ mixed step
     if "mixed" in legs:
         result["mixed_step"] = mixed_leg(torch, dev, args, orc)
@@ -602,7 +647,7 @@ def main():
         "cpu_baseline": cpu,
     }
     for k in ("kv_store", "prologue", "prefill", "spec_verify", "decode_graph", "step_metadata",
-              "mixed_step"):
+              "sampler", "mixed_step"):
         if k in result:
             line[k] = result[k]
     print(json.dumps(line), flush=True)

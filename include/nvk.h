@@ -278,6 +278,36 @@ int nvk_decode_metadata(const int32_t* seq_lens, const int32_t* bt_offsets,
                         int32_t* context_lens, int64_t* positions, int32_t* slot_mapping,
                         int32_t* block_tables, void* stream);
 
+/*
+ * LM-head last-token gather (nanovllm/layers/embed_head.py:56-60): in a
+ * prefill step, out[b] = x[cu_seqlens_q[b+1] - 1] (row b of [batch][hidden]
+ * bf16, row strides in elements).  A sequence with cu_seqlens_q[b+1] == 0
+ * leaves its output row unwritten.  hidden and strides multiples of 8.
+ */
+int nvk_gather_last_tokens(const void* x, int64_t x_row_stride, const int32_t* cu_seqlens_q,
+                           int32_t batch, int32_t hidden, int32_t dtype, void* out,
+                           int64_t out_row_stride, void* stream);
+
+/*
+ * Temperature sampling (nanovllm/layers/sampler.py:7-12):
+ *   tokens[b] = argmax_i softmax(logits[b] / temperatures[b])_i / max(E_i, 1e-10)
+ * with E_i ~ Exp(1), evaluated as argmax_i logits[b][i] / T - log max(E_i, 1e-10)
+ * (the same maximiser: the softmax normaliser is one constant per row).
+ * noise != NULL: E = noise[b][i] (float32, row stride noise_row_stride);
+ * noise == NULL: E = -ln(u), u in (0, 1] from Philox4x32-10 keyed by seed,
+ * counter (offset + i/4, b): advance offset by at least ceil(vocab/4) between
+ * calls that must draw independently.  Ties go to the smallest index.
+ * logits: bf16 or f32 [batch][row_stride]; tokens: int64 [batch].
+ * workspace: nvk_sample_workspace_size() bytes (16-byte aligned; per row and
+ * 8192-element chunk one (score, index) winner), need not be initialised.
+ * Two kernels: per-chunk winners, then one wave per row.
+ */
+size_t nvk_sample_workspace_size(int32_t batch, int32_t vocab);
+int nvk_sample(const void* logits, int64_t row_stride, int32_t batch, int32_t vocab,
+               int32_t dtype, const float* temperatures, const float* noise,
+               int64_t noise_row_stride, uint64_t seed, uint64_t offset, int64_t* tokens,
+               void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,6 +55,12 @@ SIGNATURES = {
                                             _c_ptr]),
     "nvk_decode_metadata": (ctypes.c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i32, _c_i32, _c_i32, _c_i32,
                                            _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr]),
+    "nvk_sample_workspace_size": (ctypes.c_size_t, [_c_i32, _c_i32]),
+    "nvk_sample": (ctypes.c_int, [_c_ptr, _c_i64, _c_i32, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_i64,
+                                  ctypes.c_uint64, ctypes.c_uint64, _c_ptr, _c_ptr, ctypes.c_size_t,
+                                  _c_ptr]),
+    "nvk_gather_last_tokens": (ctypes.c_int, [_c_ptr, _c_i64, _c_ptr, _c_i32, _c_i32, _c_i32, _c_ptr,
+                                              _c_i64, _c_ptr]),
 }
 
 _lib: ctypes.CDLL | None = None

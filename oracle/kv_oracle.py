@@ -23,6 +23,10 @@ What it restates (numpy, bf16 carried as uint16 bit patterns):
   qk_norm_rope_store  the prologue of Qwen3Attention.forward,
                     nanovllm/models/qwen3.py:79-86, followed by the store of
                     attention.py:62-63
+  last_token_rows   ParallelLMHead's prefill selection, embed_head.py:57-59
+  sample_tokens     Sampler.forward, nanovllm/layers/sampler.py:7-12, for a
+                    given noise tensor (softmax in float32, probs / noise
+                    clamped at 1e-10, first maximal index)
 
 How each function is pinned (tests/test_oracle.py):
   kv_store          the guide's worked store example and test matrix
@@ -51,6 +55,14 @@ How each function is pinned (tests/test_oracle.py):
                     pairs) fails these checks.
   qk_norm_rope_store  composition of the two above plus kv_store, checked
                     against a per-token loop of them.
+  last_token_rows   the guide's LM-head example (query lengths [2, 1, 4],
+                    cu_seqlens_q [0, 2, 3, 7], last indices [1, 2, 6],
+                    master_nano-vllm-v2.md:1222; tests/golden fixture).
+  sample_tokens     the exponential-race theorem (P[token = i] = softmax_i,
+                    chi-square over numpy Exp(1) draws), unit noise -> argmax
+                    of the logits, temperature scaling of the distribution;
+                    planted mistakes (noise multiplied, temperature
+                    multiplied) fail the chi-square.
 """
 from __future__ import annotations
 
@@ -58,7 +70,8 @@ import numpy as np
 
 __all__ = ["bf16_to_f32", "f32_to_bf16", "kv_store", "slots_for", "gather_rows",
            "paged_attention", "attention_bytes", "prefill_flops", "rms_norm",
-           "apply_rotary_emb", "qk_norm_rope_store", "prologue_bytes"]
+           "apply_rotary_emb", "qk_norm_rope_store", "prologue_bytes", "last_token_rows",
+           "sample_tokens"]
 
 
 # ---------------------------------------------------------------------------
@@ -269,6 +282,31 @@ def prologue_bytes(n_tokens: int, n_valid_slots: int, n_unique_positions: int,
     if write_k:
         wr += n_tokens * num_kv_heads * row
     return rd + wr
+
+
+# ---------------------------------------------------------------------------
+# LM-head last-token selection and the sampler
+# ---------------------------------------------------------------------------
+def last_token_rows(x: np.ndarray, cu_seqlens_q) -> np.ndarray:
+    """x[cu_seqlens_q[1:] - 1] (embed_head.py:57-59)."""
+    cu = np.asarray(cu_seqlens_q, dtype=np.int64)
+    return x[cu[1:] - 1]
+
+
+def sample_tokens(logits: np.ndarray, temperatures, noise: np.ndarray,
+                  _mutation: str | None = None) -> np.ndarray:
+    """sampler.py:7-12 with the Exp(1) draw given: probs = softmax(logits.float()
+    / T) in float32, probs / max(noise, 1e-10), argmax (first maximal index).
+    logits: float array or uint16 bf16 bit patterns [B, V]."""
+    x = bf16_to_f32(logits) if logits.dtype == np.uint16 else logits.astype(np.float32)
+    t = np.asarray(temperatures, dtype=np.float32)[:, None]
+    x = x * t if _mutation == "temp_mul" else x / t
+    m = x.max(axis=1, keepdims=True)
+    p = np.exp(x - m)
+    p = (p / p.sum(axis=1, keepdims=True)).astype(np.float32)
+    e = np.maximum(np.asarray(noise, dtype=np.float32), np.float32(1e-10))
+    q = p * e if _mutation == "noise_mul" else p / e
+    return np.argmax(q, axis=1).astype(np.int64)
 
 
 # ---------------------------------------------------------------------------
