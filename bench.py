@@ -599,7 +599,7 @@ def main():
         result["spec_verify"] = dict(
             ms_per_step=wall_v * 1e3, bytes_per_step=sv_bytes,
             workload="32 sequences x 6 query tokens (5 drafts + the last accepted token) over "
-                     "U{1024..8192} paged keys, split-K",
+                     "U{1024..8192} paged keys (short-query stream-K kernels)",
             roofline={"bound": "hbm", "achieved": round(sv_bytes / ev_v / 1e9, 2),
                       "peak": HBM_PEAK_GBS, "unit": "GB/s",
                       "frac": round(sv_bytes / ev_v / 1e9 / HBM_PEAK_GBS, 4),

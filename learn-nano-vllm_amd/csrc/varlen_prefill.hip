@@ -34,6 +34,7 @@
 //   * The grid runs the query tiles nearest the end of each sequence (the
 //     ones with most keys) first.
 #include "nvk_common.h"
+#include "short_query.h"
 
 namespace {
 
@@ -757,9 +758,16 @@ extern "C" size_t nvk_varlen_prefill_workspace_size(int32_t batch, int32_t max_s
     return 0;
   const int G = num_q_heads / num_kv_heads;
   if (G != 1 && G != 2 && G != 4 && G != 8) return 0;
-  return split_workspace_bytes(plan_splits(batch, max_seqlen_q, max_seqlen_k, num_q_heads,
-                                           num_kv_heads),
-                               batch, num_kv_heads);
+  const size_t split = split_workspace_bytes(
+      plan_splits(batch, max_seqlen_q, max_seqlen_k, num_q_heads, num_kv_heads), batch,
+      num_kv_heads);
+  // short query ranges over paged keys take the short-query kernels (pages of
+  // a multiple of 64 keys; the size does not depend on the page size)
+  const size_t sq = short_query_applies(true, 64, max_seqlen_q, num_q_heads, num_kv_heads,
+                                        head_dim, batch)
+                        ? short_query_ws_bytes(batch, max_seqlen_k, num_q_heads, num_kv_heads)
+                        : 0;
+  return split > sq ? split : sq;
 }
 
 extern "C" int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -806,6 +814,36 @@ extern "C" int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q
   // (paged) or the k rows (dense).
   int64_t max_keys = block_tables ? (int64_t)max_blocks * block_size : total_k;
   if (max_seqlen_k > 0 && max_seqlen_k < max_keys) max_keys = max_seqlen_k;
+
+  // Short query ranges (<= 16 rows per kv head) over paged keys: the stream-K
+  // short-query kernels, when the workspace holds their records.
+  if (num_blocks > 0 && max_keys > 0 &&
+      short_query_applies(block_tables != nullptr, block_size, max_seqlen_q, num_q_heads,
+                          num_kv_heads, head_dim, batch) &&
+      workspace && workspace_bytes >= short_query_ws_bytes(batch, max_keys, num_q_heads,
+                                                           num_kv_heads)) {
+    ShortQueryParams sp;
+    sp.q = static_cast<const uint16_t*>(q);
+    sp.q_stride_tok = q_stride_tok;
+    sp.q_stride_head = q_stride_head;
+    sp.k_cache = static_cast<const uint16_t*>(k);
+    sp.v_cache = static_cast<const uint16_t*>(v);
+    sp.cu_q = cu_seqlens_q;
+    sp.cu_k = cu_seqlens_k;
+    sp.batch = batch;
+    sp.block_tables = block_tables;
+    sp.bt_stride = bt_stride;
+    sp.max_blocks = max_blocks;
+    sp.block_size = block_size;
+    sp.num_blocks = num_blocks;
+    sp.num_q_heads = num_q_heads;
+    sp.num_kv_heads = num_kv_heads;
+    sp.scale = scale;
+    sp.out = static_cast<uint16_t*>(out);
+    sp.out_stride_tok = out_stride_tok;
+    sp.out_stride_head = out_stride_head;
+    return short_query_launch(sp, max_keys, workspace, reinterpret_cast<hipStream_t>(stream));
+  }
   SplitPlan sp = plan_splits(batch, max_seqlen_q, max_keys, num_q_heads, num_kv_heads);
   if (sp.n_qtiles > 65535) return NVK_EINVAL;
   if (sp.n_splits > 1 && (!workspace || workspace_bytes < split_workspace_bytes(sp, batch,

@@ -71,14 +71,21 @@ def test_error_codes_without_launching():
     assert lib.nvk_varlen_prefill(16, 2048, 128, 4, 16, 16, 1024, 1024, 128, 4, 16, 16, 1, 4, 4,
                                   None, 0, 0, 0, 0, 16, 8, 64, 0.1, 16, 2048, 128, None, 0, 0,
                                   None) == -2
-    # split-K workspace: 32 sequences of 6 queries over <= 8192 keys (8 kv heads x 32 x 1
-    # query tile = 256 workgroups) split 4 ways; records of 128 rows x (128 + 4) floats
-    assert lib.nvk_varlen_prefill_workspace_size(32, 6, 8192, 16, 8, 128) == \
-        8 * 32 * 1 * 4 * 128 * 132 * 4
-    # enough query tiles to fill the GPU: no split, no workspace
+    # 32 sequences of 6 queries over <= 8192 keys: the larger of the split-K records of
+    # the tile kernel (8 kv heads x 32 x 1 query tile = 256 workgroups, split 4 ways,
+    # 128 rows x (128 + 4) floats) and the short-query kernels' (descriptors + 2
+    # records of 16 rows per wave of a 2048-wave grid)
+    split = 8 * 32 * 1 * 4 * 128 * 132 * 4
+    short = 32 * 8 * 8 + 2048 * 2 * 16 * 132 * 4
+    assert lib.nvk_varlen_prefill_workspace_size(32, 6, 8192, 16, 8, 128) == max(split, short)
+    # enough query tiles to fill the GPU and too many rows for the short path: none
     assert lib.nvk_varlen_prefill_workspace_size(32, 1024, 1536, 16, 8, 128) == 0
-    # short key ranges are never split
-    assert lib.nvk_varlen_prefill_workspace_size(1, 6, 512, 16, 8, 128) == 0
+    # one sequence of 6 queries over 512 keys: no split; the short-query kernels'
+    # records for 64 chunks / 2 per wave = 32 waves
+    assert lib.nvk_varlen_prefill_workspace_size(1, 6, 512, 16, 8, 128) == \
+        256 + 32 * 2 * 16 * 132 * 4
+    # 9 queries x G 2 = 18 rows: too many for the short path
+    assert lib.nvk_varlen_prefill_workspace_size(1, 9, 512, 16, 8, 128) == 0
     # fused prologue: (qkv, stride, T, pos, qw, kw, eps, cos_sin, cs_stride, max_pos, Hq, Hkv,
     # D, q_out, strides, k_out, strides, k_cache, v_cache, slots, cache_slots, dtype, stream)
     pro = [16, 32 * 128, 4, 16, 16, 16, 1e-6, 16, 128, 4096, 16, 8, 128, 16, 16 * 128, 128,
