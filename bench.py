@@ -28,8 +28,10 @@ over four copies of the KV pool, so no step finds its working set in the
 256 MB Infinity Cache), replays it W-step-graph first as warmup, then
 brackets one replay of the K-step graph with device synchronisation (wall
 clock -> ms_per_step) and HIP events on the launch stream (-> roofline
-achieved).  The CPU baseline is the numpy oracle on one host thread, timed on
-the same inputs.
+achieved).  The CPU baseline of the store, decode and prefill legs is the
+reference's path on the host CPU in PyTorch (index_put, block-table gather +
+scaled_dot_product_attention; oracle/torch_cpu.py) on up to 16 host threads;
+the prologue's is the numpy oracle on one thread.  Both run on the same inputs.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                   [--legs decode,store,prologue,prefill,spec,graph,metadata,sampler,mixed]
@@ -137,6 +139,14 @@ def cpu_time(fn, reps):
         fn()
         ts.append(time.perf_counter() - t0)
     return statistics.median(ts)
+
+
+def host_threads(torch):
+    """Host threads the CPU baseline runs on: the CPUs this process may use,
+    at most 16 (a one-GPU box's share)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    torch.set_num_threads(max(1, min(16, n or 1)))
+    return torch.get_num_threads()
 
 
 def traffic_for(leg):
@@ -459,7 +469,6 @@ def main():
 
     import numpy as np
     import torch
-    from threadpoolctl import threadpool_limits
 
     if args.copy_calibration:
         n = args.copy_calibration << 20
@@ -475,6 +484,7 @@ def main():
     from nanovllm_amd.workloads import (decode_case, kv_store_case, prefill_case,
                                         spec_verify_case)
     from oracle import kv_oracle as orc
+    from oracle import torch_cpu as tcpu
 
     legs = set(args.legs.split(","))
     dev = torch.device("cuda:0")
@@ -500,15 +510,16 @@ def main():
                             bytes_per_step=dec_bytes)
     cpu = None
     if not args.no_cpu_baseline:
-        log("cpu baseline: decode oracle, 1 thread")
-        q, kc, vc = bits(dc.q), bits(dc.k_cache), bits(dc.v_cache)
-        lens, bt = dc.context_lens.numpy(), dc.block_tables.numpy()
-        with threadpool_limits(1):
-            t = cpu_time(lambda: orc.paged_attention(q, kc, vc, np.arange(65), lens, dc.scale,
-                                                     block_tables=bt, block_size=256), 20)
-        cpu = {"value": round(dec_bytes / t / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": "the full 64-sequence decode batch through the numpy oracle "
-                         "(gather + f32 softmax attention), median of 20 reps on 1 host thread"}
+        threads = host_threads(torch)
+        log(f"cpu baseline: decode on the PyTorch CPU path, {threads} threads")
+        t = cpu_time(lambda: tcpu.paged_attention_cpu(dc.q, dc.k_cache, dc.v_cache, range(65),
+                                                      dc.context_lens, dc.scale,
+                                                      dc.block_tables), 10)
+        cpu = {"value": round(dec_bytes / t / 1e9, 4), "unit": "GB/s", "cores": threads,
+               "kind": "port",
+               "sample": "the full 64-sequence decode batch through the PyTorch CPU path "
+                         "(block-table gather + f32 scaled_dot_product_attention), median of "
+                         f"10 reps on {threads} host threads"}
     del pools, outs, dec_fns
 
     # ------------------------------------------------------------------ store
@@ -528,17 +539,15 @@ def main():
                              "frac": round(st_bytes / ev_s / 1e9 / HBM_PEAK_GBS, 4),
                              "traffic": traffic_for("kv_store")})
         if not args.no_cpu_baseline:
-            kb, vb, sl = bits(sc.key), bits(sc.value), sc.slot_mapping.numpy()
-            kc0, vc0 = bits(sc.k_cache), bits(sc.v_cache)
-
-            def cpu_store():
-                kc, vc = kc0.copy(), vc0.copy()
-                orc.kv_store(kb, vb, kc, vc, sl)
-            t = cpu_time(cpu_store, 50)
+            threads = host_threads(torch)
+            kc, vc = sc.k_cache.clone(), sc.v_cache.clone()
+            t = cpu_time(lambda: tcpu.store_kvcache_cpu(sc.key, sc.value, kc, vc,
+                                                        sc.slot_mapping), 50)
             leg["cpu_baseline"] = {"value": round(st_bytes / t / 1e9, 3), "unit": "GB/s",
-                                   "cores": 1, "kind": "port",
-                                   "sample": "full 4096-token store via numpy index assignment "
-                                             "(cache copy included), median of 50 reps"}
+                                   "cores": threads, "kind": "port",
+                                   "sample": "full 4096-token store through the PyTorch CPU "
+                                             "path (index_put on the flat cache views), median "
+                                             f"of 50 reps on {threads} host threads"}
         result["kv_store"] = leg
         del copies, st_fns
 
@@ -567,16 +576,19 @@ def main():
                              "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                              "traffic": traffic_for("prefill")})
         if not args.no_cpu_baseline:
-            kc, vc = bits(pc.k_cache).copy(), bits(pc.v_cache).copy()
-            orc.kv_store(bits(pc.key), bits(pc.value), kc, vc, pc.slot_mapping.numpy())
-            qb, cuq, bt = bits(pc.q), pc.cu_seqlens_q.numpy(), pc.block_tables.numpy()
-            with threadpool_limits(1):
-                t = cpu_time(lambda: orc.paged_attention(qb, kc, vc, cuq, pc.lens_k, pc.scale,
-                                                         block_tables=bt, block_size=256), 3)
+            threads = host_threads(torch)
+            kc, vc = pc.k_cache.clone(), pc.v_cache.clone()
+            tcpu.store_kvcache_cpu(pc.key, pc.value, kc, vc, pc.slot_mapping)
+            t = cpu_time(lambda: tcpu.paged_attention_cpu(pc.q, kc, vc, pc.cu_seqlens_q,
+                                                          pc.lens_k, pc.scale,
+                                                          pc.block_tables), 5)
             leg["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
-                                   "cores": 1, "kind": "port",
-                                   "sample": "the full 32-sequence prefill through the numpy "
-                                             "oracle, median of 3 reps on 1 host thread"}
+                                   "cores": threads, "kind": "port",
+                                   "sample": "the full 32-sequence prefill through the PyTorch "
+                                             "CPU path (block-table gather + f32 "
+                                             "scaled_dot_product_attention with the "
+                                             "bottom-right causal mask), median of 5 reps on "
+                                             f"{threads} host threads"}
         result["prefill"] = leg
         del copies, outs, pf_fns
 
