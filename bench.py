@@ -23,9 +23,10 @@ decodes over U{256..4096}; a separate KV pool per layer) as the fraction of
 its roofline time (decode and store bytes at HBM peak + prefill FLOPs at MFMA
 peak).
 
-Timing: each leg builds K steps into one HIP graph (the decode steps cycle
-over four copies of the KV pool, so no step finds its working set in the
-256 MB Infinity Cache), replays it W-step-graph first as warmup, then
+Timing: each leg builds K steps into one HIP graph cycling over copies of its
+inputs (as many as make one cycle touch >= 1 GiB, 4x the 256 MB Infinity
+Cache, so no step finds its working set cached from the previous use of its
+copy), replays a W-step graph first as warmup, then
 brackets one replay of the K-step graph with device synchronisation (wall
 clock -> ms_per_step) and HIP events on the launch stream (-> roofline
 achieved).  The CPU baseline of the store, decode and prefill legs is the
@@ -103,7 +104,7 @@ def time_graph(torch, step_fns, steps, warmup, eager=False):
     (wall seconds per step, event seconds per step)."""
     if eager:
         return time_eager(torch, step_fns, steps, warmup)
-    def capture(n):
+    def capture(n, start):
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -113,11 +114,12 @@ def time_graph(torch, step_fns, steps, warmup, eager=False):
         torch.cuda.current_stream().wait_stream(s)
         with torch.cuda.graph(g):
             for i in range(n):
-                step_fns[i % len(step_fns)]()
+                step_fns[(start + i) % len(step_fns)]()
         return g
 
-    g_warm = capture(max(1, warmup))
-    g = capture(steps)
+    # the timed steps continue the cycle where the warmup stopped
+    g_warm = capture(max(1, warmup), 0)
+    g = capture(steps, max(1, warmup) % len(step_fns))
     g_warm.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -139,6 +141,16 @@ def cpu_time(fn, reps):
         fn()
         ts.append(time.perf_counter() - t0)
     return statistics.median(ts)
+
+
+MALL_CYCLE_BYTES = 1 << 30   # 4x the 256 MB Infinity Cache
+
+
+def rotation(bytes_per_call, least=2):
+    """Copies of a leg's inputs to cycle over so that one cycle touches at least
+    1 GiB of distinct data: no call finds its working set still in the 256 MB
+    Infinity Cache from the previous use of the same copy."""
+    return max(least, -(-MALL_CYCLE_BYTES // max(1, int(bytes_per_call))))
 
 
 def host_threads(torch):
@@ -215,7 +227,7 @@ def mixed_leg(torch, dev, args, orc, layers=28):
 
 def prologue_leg(torch, dev, args, orc, bits):
     """Fused q/k RMSNorm + RoPE + KV-store over the mixed step's 4288 new tokens
-    of one layer (4 rotated copies of qkv and of the 3300-page caches), and the
+    of one layer (rotated copies of the inputs storing into one 3300-page pool), and the
     same steps as separate eager torch operations (the reference's
     layernorm.py:16-26 / rotary_embedding.py:6-14 code, then the store) for
     comparison."""
@@ -227,11 +239,21 @@ def prologue_leg(torch, dev, args, orc, bits):
     log("building prologue workload (4288 tokens of the mixed step, 3300-page pool)")
     pc = prologue_case()
     hq, hkv, hd, eps = pc.hq, pc.hkv, pc.hd, pc.eps
+    n_valid = int((pc.slot_mapping >= 0).sum())
+    pbytes = orc.prologue_bytes(pc.n_tokens, n_valid, pc.n_unique_positions, hq, hkv, hd,
+                                write_k=False)
+    # copies of the step's inputs; every copy stores into other rows of one
+    # shared pool (its slots shifted by a multiple of 53 pages, mod the pool)
+    kc = torch.zeros(pc.pool_blocks, pc.block_size, hkv, hd, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    n_slots = pc.pool_blocks * pc.block_size
     copies = []
-    for _ in range(4):
+    for i in range(rotation(pbytes)):
         c = pc.to(dev)
-        kc = torch.zeros(pc.pool_blocks, pc.block_size, hkv, hd, dtype=torch.bfloat16, device=dev)
-        copies.append((c, kc, torch.zeros_like(kc)))
+        sm = c.slot_mapping
+        c.tensors["slot_mapping"] = torch.where(sm >= 0, (sm + i * 53 * pc.block_size) % n_slots,
+                                                sm)
+        copies.append((c, kc, vc))
     fused = [(lambda c=c, kc=kc, vc=vc: qk_norm_rope_store(
         c.positions, c.qkv, hq, hkv, hd, c.q_weight, c.k_weight, eps, c.cos_sin, kc, vc,
         c.slot_mapping, return_k=False)) for c, kc, vc in copies]
@@ -257,9 +279,6 @@ def prologue_leg(torch, dev, args, orc, bits):
         return q
 
     unfused = [(lambda c=c, kc=kc, vc=vc: unfused_step(c, kc, vc)) for c, kc, vc in copies]
-    n_valid = int((pc.slot_mapping >= 0).sum())
-    pbytes = orc.prologue_bytes(pc.n_tokens, n_valid, pc.n_unique_positions, hq, hkv, hd,
-                                write_k=False)
     log("timing fused prologue")
     wall, ev = time_graph(torch, fused, args.steps, args.warmup, args.eager)
     log("timing the same steps as eager torch operations")
@@ -439,10 +458,10 @@ def sampler_leg(torch, dev, args):
 
     for b in (64, 512):
         gen = torch.Generator(device=dev).manual_seed(b)
-        logits = [(torch.randn(b, vocab, generator=gen, device=dev) * 3).to(torch.bfloat16)
-                  for _ in range(4)]
-        temps = torch.full((b,), 0.8, device=dev)
         nbytes = b * vocab * 2 + b * 8
+        logits = [(torch.randn(b, vocab, generator=gen, device=dev) * 3).to(torch.bfloat16)
+                  for _ in range(rotation(nbytes))]
+        temps = torch.full((b,), 0.8, device=dev)
         fused = [(lambda x=x: sampler(x, temps)) for x in logits]
         ref = [(lambda x=x: torch_sampler(x, temps)) for x in logits]
         log(f"timing sampler B={b}")
@@ -495,13 +514,13 @@ def main():
     # ------------------------------------------------------------------ decode
     log("building decode workload (B=64, ctx U{100..2048}, 1024-page pool)")
     dc = decode_case()
-    pools = [dc.to(dev)] + [dc.to(dev) for _ in range(3)]   # four separate copies
+    dec_bytes = orc.attention_bytes(dc.lens, 8, 128, 64, 16)
+    pools = [dc.to(dev) for _ in range(rotation(dec_bytes))]   # separate copies of the pool
     outs = [torch.empty(64, 16, 128, dtype=torch.bfloat16, device=dev) for _ in pools]
     dec_fns = [
         (lambda c=c, o=o: paged_decode(c.q, c.k_cache, c.v_cache, c.context_lens,
                                        c.block_tables, dc.scale, out=o))
         for c, o in zip(pools, outs)]
-    dec_bytes = orc.attention_bytes(dc.lens, 8, 128, 64, 16)
     log("timing decode")
     wall, ev = time_graph(torch, dec_fns, args.steps, args.warmup, args.eager)
     dec_gbs = dec_bytes / wall / 1e9
@@ -526,11 +545,11 @@ def main():
     if "store" in legs:
         log("building kv-store workload (4096 tokens, 64 pages, 205 slots -1)")
         sc = kv_store_case()
-        copies = [sc.to(dev) for _ in range(4)]
-        st_fns = [(lambda c=c: store_kvcache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping))
-                  for c in copies]
         n_valid = int((sc.slot_mapping >= 0).sum())
         st_bytes = n_valid * 2 * 2 * 8 * 128 * 2 + 4 * 4096
+        copies = [sc.to(dev) for _ in range(rotation(st_bytes))]
+        st_fns = [(lambda c=c: store_kvcache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping))
+                  for c in copies]
         log("timing kv-store")
         wall_s, ev_s = time_graph(torch, st_fns, args.steps, args.warmup, args.eager)
         leg = dict(ms_per_step=wall_s * 1e3, bytes_per_step=st_bytes,
@@ -559,7 +578,8 @@ def main():
     if "prefill" in legs:
         log("building prefill workload (32 seqs, 512-token shared prefix)")
         pc = prefill_case()
-        copies = [pc.to(dev) for _ in range(2)]
+        touched = orc.attention_bytes(pc.lens_k, 8, 128, sum(pc.lens_q), 16)
+        copies = [pc.to(dev) for _ in range(rotation(touched))]
         for c in copies:   # the new tokens' K/V are in the cache before attention
             store_kvcache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping)
         outs = [torch.empty_like(c.q) for c in copies]
@@ -596,7 +616,8 @@ def main():
     if "spec" in legs:
         log("building spec-verify workload (32 seqs, 6 queries, ctx U{1024..8192})")
         vc_ = spec_verify_case()
-        copies = [vc_.to(dev) for _ in range(2)]
+        sv_bytes = orc.attention_bytes(vc_.lens_k, 8, 128, 32 * 6, 16)
+        copies = [vc_.to(dev) for _ in range(rotation(sv_bytes))]
         for c in copies:   # the 5 draft tokens of every sequence are stored first
             store_kvcache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping)
         outs = [torch.empty_like(c.q) for c in copies]
@@ -605,7 +626,6 @@ def main():
                                                    block_table=c.block_tables, out=o,
                                                    max_seqlen_k=vc_.max_seqlen_k))
                   for c, o in zip(copies, outs)]
-        sv_bytes = orc.attention_bytes(vc_.lens_k, 8, 128, 32 * 6, 16)
         log("timing spec verify")
         wall_v, ev_v = time_graph(torch, sv_fns, args.steps, args.warmup, args.eager)
         result["spec_verify"] = dict(

@@ -57,6 +57,19 @@ struct PrologueArgs {
   int64_t cache_slots;
 };
 
+// The qkv rows are read once and every output row (q, k, cache rows) written
+// once per step: non-temporal 16-byte accesses.  Measured on one layer of the
+// mixed step (4288 tokens, inputs cycling through more than the Infinity
+// Cache): 19.3 us cached, 17.7 us non-temporal; non-temporal loads or cache
+// stores alone change nothing.  The cos/sin rows are shared by the tokens of a
+// position and stay cached.
+__device__ __forceinline__ nvk_u32x4 load_nt(const uint16_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const nvk_u32x4*>(p));
+}
+__device__ __forceinline__ void store_nt(uint16_t* p, nvk_u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<nvk_u32x4*>(p));
+}
+
 __device__ __forceinline__ float bf16_round(float x) {
   return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) << 16);
 }
@@ -65,8 +78,7 @@ __device__ __forceinline__ float bf16_round(float x) {
 __device__ __forceinline__ void prologue_row(const PrologueArgs& a, int64_t t, int r, int j,
                                              int64_t pos, int32_t slot) {
 #pragma clang fp contract(off)
-  const nvk_u32x4 raw =
-      *reinterpret_cast<const nvk_u32x4*>(a.qkv + t * a.qkv_row_stride + (int64_t)r * kHD + 8 * j);
+  const nvk_u32x4 raw = load_nt(a.qkv + t * a.qkv_row_stride + (int64_t)r * kHD + 8 * j);
   const bool is_q = r < a.num_q_heads;
   const bool is_k = !is_q && r < a.num_q_heads + a.num_kv_heads;
 
@@ -75,7 +87,7 @@ __device__ __forceinline__ void prologue_row(const PrologueArgs& a, int64_t t, i
   if (!is_q && !is_k) {  // v row: a plain copy into the cache
     if (slot >= 0) {
       const int kvh = r - a.num_q_heads - a.num_kv_heads;
-      *reinterpret_cast<nvk_u32x4*>(a.v_cache + (int64_t)slot * row_elems + kvh * kHD + 8 * j) = raw;
+      store_nt(a.v_cache + (int64_t)slot * row_elems + kvh * kHD + 8 * j, raw);
     }
     return;
   }
@@ -127,16 +139,14 @@ __device__ __forceinline__ void prologue_row(const PrologueArgs& a, int64_t t, i
   outw.z = nvk_pack_bf16x2(y[4], y[5]);
   outw.w = nvk_pack_bf16x2(y[6], y[7]);
   if (is_q) {
-    *reinterpret_cast<nvk_u32x4*>(a.q_out + t * a.q_out_stride_tok + (int64_t)r * a.q_out_stride_head +
-                                  8 * j) = outw;
+    store_nt(a.q_out + t * a.q_out_stride_tok + (int64_t)r * a.q_out_stride_head + 8 * j, outw);
     return;
   }
   const int kvh = r - a.num_q_heads;
   if (a.k_out != nullptr)
-    *reinterpret_cast<nvk_u32x4*>(a.k_out + t * a.k_out_stride_tok + (int64_t)kvh * a.k_out_stride_head +
-                                  8 * j) = outw;
+    store_nt(a.k_out + t * a.k_out_stride_tok + (int64_t)kvh * a.k_out_stride_head + 8 * j, outw);
   if (slot >= 0)
-    *reinterpret_cast<nvk_u32x4*>(a.k_cache + (int64_t)slot * row_elems + kvh * kHD + 8 * j) = outw;
+    store_nt(a.k_cache + (int64_t)slot * row_elems + kvh * kHD + 8 * j, outw);
 }
 
 
