@@ -35,10 +35,14 @@ struct U4 {
   uint32_t x, y, z, w;
 };
 
+// hi(p1) ^ c.y ^ k0 and hi(p0) ^ c.w ^ k1 as one three-input v_bitop3_b32 each
+// (truth table 0x96 = a ^ b ^ c); the 32x32->64 products are v_mad_u64_u32.
 __device__ __forceinline__ U4 philox_round(U4 c, uint32_t k0, uint32_t k1) {
   const uint64_t p0 = (uint64_t)0xD2511F53u * c.x;
   const uint64_t p1 = (uint64_t)0xCD9E8D57u * c.z;
-  return U4{(uint32_t)(p1 >> 32) ^ c.y ^ k0, (uint32_t)p1, (uint32_t)(p0 >> 32) ^ c.w ^ k1,
+  return U4{(uint32_t)__builtin_amdgcn_bitop3_b32((uint32_t)(p1 >> 32), c.y, k0, 0x96),
+            (uint32_t)p1,
+            (uint32_t)__builtin_amdgcn_bitop3_b32((uint32_t)(p0 >> 32), c.w, k1, 0x96),
             (uint32_t)p0};
 }
 
