@@ -538,7 +538,8 @@ def main():
                "kind": "port",
                "sample": "the full 64-sequence decode batch through the PyTorch CPU path "
                          "(block-table gather + f32 scaled_dot_product_attention), median of "
-                         f"10 reps on {threads} host threads"}
+                         f"10 reps on {threads} host threads "
+                         f"(os.cpu_count() = {os.cpu_count()})"}
     del pools, outs, dec_fns
 
     # ------------------------------------------------------------------ store
@@ -566,7 +567,8 @@ def main():
                                    "cores": threads, "kind": "port",
                                    "sample": "full 4096-token store through the PyTorch CPU "
                                              "path (index_put on the flat cache views), median "
-                                             f"of 50 reps on {threads} host threads"}
+                                             f"of 50 reps on {threads} host threads "
+                                             f"(os.cpu_count() = {os.cpu_count()})"}
         result["kv_store"] = leg
         del copies, st_fns
 
@@ -608,7 +610,8 @@ def main():
                                              "CPU path (block-table gather + f32 "
                                              "scaled_dot_product_attention with the "
                                              "bottom-right causal mask), median of 5 reps on "
-                                             f"{threads} host threads"}
+                                             f"{threads} host threads "
+                                             f"(os.cpu_count() = {os.cpu_count()})"}
         result["prefill"] = leg
         del copies, outs, pf_fns
 
