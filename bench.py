@@ -314,7 +314,9 @@ def decode_graph_leg(torch, dev, args, orc, layers=28):
     """The decode attention path of a 28-layer Qwen3-0.6B stack, captured per
     batch bucket and replayed as the reference's run_model does: per layer the
     fused prologue (q/k norms, rotation, store of the new token) and the paged
-    decode over config 2's contexts (B = 64, U{100..2048}); every layer has
+    decode over the headline decode contexts (B = 64, U{100..2048}; the B = 4 line
+    runs both inside the decode kernel, as attention_with_prologue routes
+    batches of up to 32); every layer has
     its own 1024-page cache (views of one [2, 28, 1024, 256, 8, 128]
     allocation).  Timed as graph replays (run() with its host-side buffer
     refresh) and as the same step launched eagerly."""

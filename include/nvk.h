@@ -20,6 +20,8 @@
  *   nvk_qk_norm_rope_store <- q_norm / k_norm / rotary_emb of Qwen3Attention.forward
  *                          (nanovllm/models/qwen3.py:79-86) + the store of
  *                          attention.py:62-63
+ *   nvk_paged_decode_prologue <- the same prologue + the decode call of a
+ *                          decode step, in one decode kernel
  *
  * Conventions shared by every entry point
  *   - All pointers are device pointers (hipMalloc / torch CUDA tensors) except
@@ -236,6 +238,34 @@ int nvk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, int64_t n_to
                            void* k_out, int64_t k_out_stride_tok, int64_t k_out_stride_head,
                            void* k_cache, void* v_cache, const int32_t* slot_mapping,
                            int64_t cache_slots, int32_t dtype, void* stream);
+
+/*
+ * Decode step with the attention prologue applied inside the decode kernel:
+ * nvk_qk_norm_rope_store followed by nvk_paged_decode for one new token per
+ * sequence (qwen3.py:79-86 then attention.py:62-63 and 72-74 in a decode
+ * step), without materialising q and with one launch fewer.
+ * Row b of qkv is sequence b's new token (row stride qkv_row_stride, layout
+ * as in nvk_qk_norm_rope_store).  q is normed and rotated at positions[b] in
+ * the kernel; the new token's k (normed, rotated) and v are stored at cache
+ * row slot_mapping[b] (skipped when outside [0, cache_slots)) and used from
+ * registers for key context_lens[b] - 1, which must be that cache row (as
+ * model_runner.prepare_decode builds it: slot = the row of position
+ * len - 1, context_lens = len); a sequence of context length 0 (a graph
+ * padding row) stores nothing.  Output, caches, block tables, context
+ * lengths, workspace (nvk_paged_decode_workspace_size) and empty contexts as
+ * in nvk_paged_decode; norm weights, eps, cos_sin_cache and positions as in
+ * nvk_qk_norm_rope_store.  The result equals the two calls' bit for bit.
+ * head_dim: 128.  Two kernels are enqueued (decode with prologue, combine).
+ */
+int nvk_paged_decode_prologue(
+    const void* qkv, int64_t qkv_row_stride, const int64_t* positions, const void* q_norm_weight,
+    const void* k_norm_weight, float eps, const float* cos_sin_cache, int64_t cos_sin_row_stride,
+    int64_t max_position, void* k_cache, void* v_cache, const int32_t* slot_mapping,
+    int64_t cache_slots, const int32_t* block_tables, int64_t bt_stride,
+    const int32_t* context_lens, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int32_t max_blocks, int32_t num_blocks, float scale,
+    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+    size_t workspace_bytes, int32_t dtype, void* stream);
 
 /*
  * Device-side step metadata.

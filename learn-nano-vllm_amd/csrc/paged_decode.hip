@@ -43,6 +43,7 @@
 // empty contexts.  (Merging inside the main kernel needs cross-XCD release /
 // acquire fences per part; on MI355X those cost far more than the combine.)
 #include "nvk_common.h"
+#include "qk_math.h"
 
 namespace {
 
@@ -56,6 +57,7 @@ constexpr int kMaxBatch = 2048;    // sequences per call (LDS prefix table)
 constexpr int kMinChunks = 2;
 
 typedef __attribute__((address_space(4))) const int32_t nvk_const_i32;
+typedef __attribute__((address_space(4))) const int64_t nvk_const_i64;
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -75,6 +77,22 @@ struct DecodeArgs {
   int n_waves;       // P: waves of the grid
   int hpi;           // kv heads per load instruction
   int tc;            // tokens per chunk
+  // Fused prologue (nvk_paged_decode_prologue, head_dim 128): q and the new
+  // token's k and v come from the packed qkv row of each sequence (RMSNorm +
+  // rotary embedding of q and k at positions[b]); the new k and v are stored
+  // at slot_mapping[b] and used from registers for key context_lens[b] - 1.
+  const uint16_t* qkv;
+  int64_t qkv_row_stride;
+  const int64_t* positions;
+  const uint16_t* q_weight;
+  const uint16_t* k_weight;
+  float eps;
+  const float* cos_sin;
+  int64_t cos_sin_stride, max_position;
+  const int32_t* slot_mapping;
+  int64_t cache_slots;
+  uint16_t* k_store;  // the caches, written at the slots
+  uint16_t* v_store;
 };
 
 // context_lens and block_tables are read-only for the whole launch: read them
@@ -181,19 +199,24 @@ struct LaneRole {
 // whatever the data (no branches).  A row that does not exist (past the
 // context, or a page id outside the pool) reads this lane's q row instead: it
 // is finite, and its probability is masked to exactly 0 by the scores.
-template <int HD, int G, bool ALIGNED>
+template <int HD, int G, bool ALIGNED, bool FUSED>
 __device__ __forceinline__ void load_chunk(const DecodeArgs& a, const ChunkPos& p, int ctx,
                                            const LaneRole& r, int tpi, ChunkBuf<HD, G>& buf) {
   const int64_t row_elems = (int64_t)a.num_kv_heads * HD;
   const int kvh = p.blk * a.hpi + r.hh;
   const int64_t head_off = (int64_t)kvh * HD + 8 * r.j;
   const int base = p.k * a.tc;  // < ctx: p is a chunk of the group
-  const uint16_t* q0 = a.q + (int64_t)p.b * a.q_stride_tok +
-                       (int64_t)(kvh * G) * a.q_stride_head + 8 * r.j;
+  // the q row (fused: the raw q row of the packed qkv row) doubles as the
+  // finite source of rows that do not exist
+  const uint16_t* q0 =
+      FUSED ? a.qkv + (int64_t)p.b * a.qkv_row_stride + (int64_t)(kvh * G) * HD + 8 * r.j
+            : a.q + (int64_t)p.b * a.q_stride_tok + (int64_t)(kvh * G) * a.q_stride_head + 8 * r.j;
+  if constexpr (!FUSED) {
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const nvk_u32x4 v = *reinterpret_cast<const nvk_u32x4*>(q0 + h * a.q_stride_head);
-    buf.q[h][0] = v.x; buf.q[h][1] = v.y; buf.q[h][2] = v.z; buf.q[h][3] = v.w;
+    for (int h = 0; h < G; ++h) {
+      const nvk_u32x4 v = *reinterpret_cast<const nvk_u32x4*>(q0 + h * a.q_stride_head);
+      buf.q[h][0] = v.x; buf.q[h][1] = v.y; buf.q[h][2] = v.z; buf.q[h][3] = v.w;
+    }
   }
   const int64_t bt_off = (int64_t)p.b * a.bt_stride;
   if constexpr (ALIGNED) {
@@ -225,6 +248,73 @@ __device__ __forceinline__ void load_chunk(const DecodeArgs& a, const ChunkPos& 
       const uint16_t* vp = ok ? a.v_cache + off : q0;
       buf.k[i] = __builtin_nontemporal_load(reinterpret_cast<const nvk_u32x4*>(kp));
       buf.v[i] = __builtin_nontemporal_load(reinterpret_cast<const nvk_u32x4*>(vp));
+    }
+  }
+}
+
+// Fused prologue, head_dim 128 (16 lanes per head row, lane j = r.j).  Its
+// loads are issued before the chunk's K/V loads and its arithmetic runs after
+// them, so that its round trip overlaps the chunk's (loads complete in issue
+// order for the wait counter, so the arithmetic waits for its own loads only).
+// The computed q goes to the wave's LDS slice sq[h * 16 + j] and is read back
+// for every chunk, as the plain kernel reads q from memory; the new token's k
+// and v replace the cache rows read for key ctx - 1.
+template <int G>
+struct FusedIn {
+  nvk_u32x4 q[G], qw;        // raw q rows of the G heads, q norm weight
+  nvk_u32x4 k, kw, v;        // the new token's raw k row, k norm weight, v row
+  nvk_u32x4 cs[4];           // cos (2) and sin (2) of the lane's 8 dims
+};
+template <int HD, int G>
+__device__ __forceinline__ void fused_load(const DecodeArgs& a, int b, int64_t pos, int kvh,
+                                           bool need_q, bool need_new, const LaneRole& r,
+                                           FusedIn<G>& in) {
+  pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);
+  const float* c = a.cos_sin + pos * a.cos_sin_stride + 8 * (r.j & 7);
+  in.cs[0] = *reinterpret_cast<const nvk_u32x4*>(c);
+  in.cs[1] = *reinterpret_cast<const nvk_u32x4*>(c + 4);
+  in.cs[2] = *reinterpret_cast<const nvk_u32x4*>(c + nvk_qk::kHD / 2);
+  in.cs[3] = *reinterpret_cast<const nvk_u32x4*>(c + nvk_qk::kHD / 2 + 4);
+  const uint16_t* row = a.qkv + (int64_t)b * a.qkv_row_stride + 8 * r.j;
+  if (need_q) {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+      in.q[h] = *reinterpret_cast<const nvk_u32x4*>(row + (int64_t)(kvh * G + h) * HD);
+    in.qw = *reinterpret_cast<const nvk_u32x4*>(a.q_weight + 8 * r.j);
+  }
+  if (need_new) {
+    in.k = *reinterpret_cast<const nvk_u32x4*>(row + (int64_t)(a.num_q_heads + kvh) * HD);
+    in.v = *reinterpret_cast<const nvk_u32x4*>(
+        row + (int64_t)(a.num_q_heads + a.num_kv_heads + kvh) * HD);
+    in.kw = *reinterpret_cast<const nvk_u32x4*>(a.k_weight + 8 * r.j);
+  }
+}
+template <int HD, int G>
+__device__ __forceinline__ void fused_apply(const DecodeArgs& a, const FusedIn<G>& in, int b,
+                                            int kvh, int slot, bool need_q, bool need_new, int base,
+                                            int ctx, int tpi, const LaneRole& r, nvk_u32x4* sq,
+                                            ChunkBuf<HD, G>& buf) {
+  if (need_q) {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+      sq[h * nvk_qk::kLanesPerRow + r.j] = nvk_qk::norm_rope8_cs(in.q[h], in.qw, a.eps, in.cs, r.j);
+  }
+  if (need_new) {
+    const nvk_u32x4 kn = nvk_qk::norm_rope8_cs(in.k, in.kw, a.eps, in.cs, r.j);
+    const int rel = ctx - 1 - base;
+    const int i_new = rel / tpi, tt_new = rel % tpi;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      if (i == i_new && r.tt == tt_new) {
+        buf.k[i] = kn;
+        buf.v[i] = in.v;
+      }
+    }
+    // row group 0 stores the new token's k and v at its slot
+    if (r.tt == 0 && slot >= 0 && (int64_t)slot < a.cache_slots) {
+      const int64_t off = (int64_t)slot * a.num_kv_heads * HD + (int64_t)kvh * HD + 8 * r.j;
+      __builtin_nontemporal_store(kn, reinterpret_cast<nvk_u32x4*>(a.k_store + off));
+      __builtin_nontemporal_store(in.v, reinterpret_cast<nvk_u32x4*>(a.v_store + off));
     }
   }
 }
@@ -334,13 +424,14 @@ __device__ __forceinline__ void store_bf16x8(uint16_t* p, const float* v, float 
   *reinterpret_cast<nvk_u32x4*>(p) = w;
 }
 
-template <int HD, int G, bool ALIGNED>
+template <int HD, int G, bool ALIGNED, bool FUSED>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   using CB = ChunkBuf<HD, G>;
   constexpr int RPI = 64 / CB::LPR;           // head rows per load instruction
   constexpr int REC_HEAD = G * (HD + 4);      // floats per head in a record
   __shared__ int s_cs[kMaxBatch + 1];
   __shared__ int s_wsum[kWavesPerWG];
+  __shared__ nvk_u32x4 s_q[FUSED ? kWavesPerWG * G * nvk_qk::kLanesPerRow : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -383,12 +474,33 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   cur.k = uniform(r % cur.n);
   bool started_here = cur.k == 0;
   int ctx = clamp_ctx(a, cur.b);
+  // fused: the new token's position (a scalar read beside the context length)
+  int64_t pos = FUSED ? ((nvk_const_i64*)a.positions)[cur.b] : 0;
+  int slot = FUSED ? ((nvk_const_i32*)a.slot_mapping)[cur.b] : -1;
 
   SoftmaxState<G> st;
   st.reset();
   CB buf;
   for (int64_t c = c0;; ++c) {
-    load_chunk<HD, G, ALIGNED>(a, cur, ctx, role, tpi, buf);
+    if constexpr (FUSED) {
+      const bool need_q = c == c0 || cur.k == 0;
+      const bool need_new = cur.k == cur.n - 1;
+      const int kvh = cur.blk * hpi + role.hh;
+      nvk_u32x4* sq = s_q + (tid >> 6) * G * nvk_qk::kLanesPerRow;
+      FusedIn<G> in;
+      if (need_q || need_new) fused_load<HD, G>(a, cur.b, pos, kvh, need_q, need_new, role, in);
+      load_chunk<HD, G, ALIGNED, FUSED>(a, cur, ctx, role, tpi, buf);
+      if (need_q || need_new)
+        fused_apply<HD, G>(a, in, cur.b, kvh, slot, need_q, need_new, cur.k * a.tc, ctx, tpi, role, sq,
+                           buf);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const nvk_u32x4 v = sq[h * nvk_qk::kLanesPerRow + role.j];
+        buf.q[h][0] = v.x; buf.q[h][1] = v.y; buf.q[h][2] = v.z; buf.q[h][3] = v.w;
+      }
+    } else {
+      load_chunk<HD, G, ALIGNED, FUSED>(a, cur, ctx, role, tpi, buf);
+    }
     compute_chunk<HD, G>(a, buf, cur.k * a.tc, ctx, tpi, role, st);
     const bool last = c + 1 == c1;
     const bool group_end = cur.k == cur.n - 1;
@@ -433,7 +545,13 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     if (last) return;
     const int b_prev = cur.b;
     advance(cur, s_cs, n_blk);
-    if (cur.b != b_prev) ctx = clamp_ctx(a, cur.b);
+    if (cur.b != b_prev) {
+      ctx = clamp_ctx(a, cur.b);
+      if constexpr (FUSED) {
+        pos = ((nvk_const_i64*)a.positions)[cur.b];
+        slot = ((nvk_const_i32*)a.slot_mapping)[cur.b];
+      }
+    }
   }
 }
 
@@ -528,13 +646,13 @@ size_t decode_ws_bytes(int batch, int num_q_heads, int num_kv_heads, int head_di
   return desc + P * 2 * hpi * G * (head_dim + 4) * sizeof(float);
 }
 
-template <int HD, int G>
+template <int HD, int G, bool FUSED = false>
 int launch_decode(const DecodeArgs& a, bool aligned, hipStream_t stream) {
   const dim3 grid(a.n_waves / kWavesPerWG);
   if (aligned)
-    hipLaunchKernelGGL((paged_decode_kernel<HD, G, true>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((paged_decode_kernel<HD, G, true, FUSED>), grid, dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL((paged_decode_kernel<HD, G, false>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((paged_decode_kernel<HD, G, false, FUSED>), grid, dim3(256), 0, stream, a);
   int st = nvk_launch_status();
   if (st != NVK_OK) return st;
   hipLaunchKernelGGL((paged_decode_combine_kernel<HD, G>), dim3(a.num_kv_heads, a.batch),
@@ -542,13 +660,13 @@ int launch_decode(const DecodeArgs& a, bool aligned, hipStream_t stream) {
   return nvk_launch_status();
 }
 
-template <int HD>
+template <int HD, bool FUSED = false>
 int dispatch_group(const DecodeArgs& a, int G, bool aligned, hipStream_t s) {
   switch (G) {
-    case 1: return launch_decode<HD, 1>(a, aligned, s);
-    case 2: return launch_decode<HD, 2>(a, aligned, s);
-    case 4: return launch_decode<HD, 4>(a, aligned, s);
-    case 8: return launch_decode<HD, 8>(a, aligned, s);
+    case 1: return launch_decode<HD, 1, FUSED>(a, aligned, s);
+    case 2: return launch_decode<HD, 2, FUSED>(a, aligned, s);
+    case 4: return launch_decode<HD, 4, FUSED>(a, aligned, s);
+    case 8: return launch_decode<HD, 8, FUSED>(a, aligned, s);
     default: return NVK_EUNSUPPORTED;
   }
 }
@@ -601,7 +719,7 @@ extern "C" int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_s
   if (workspace == nullptr || workspace_bytes < need) return NVK_EWORKSPACE;
   if ((uintptr_t)workspace % 256) return NVK_EALIGN;
 
-  DecodeArgs a;
+  DecodeArgs a = {};
   a.q = static_cast<const uint16_t*>(q);
   a.q_stride_tok = q_stride_tok;
   a.q_stride_head = q_stride_head;
@@ -631,4 +749,86 @@ extern "C" int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_s
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (head_dim == 128) return dispatch_group<128>(a, G, aligned, s);
   return dispatch_group<64>(a, G, aligned, s);
+}
+
+extern "C" int nvk_paged_decode_prologue(
+    const void* qkv, int64_t qkv_row_stride, const int64_t* positions, const void* q_norm_weight,
+    const void* k_norm_weight, float eps, const float* cos_sin_cache, int64_t cos_sin_row_stride,
+    int64_t max_position, void* k_cache, void* v_cache, const int32_t* slot_mapping,
+    int64_t cache_slots, const int32_t* block_tables, int64_t bt_stride,
+    const int32_t* context_lens, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int32_t max_blocks, int32_t num_blocks, float scale,
+    void* out, int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+    size_t workspace_bytes, int32_t dtype, void* stream) {
+  if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 || max_blocks <= 0 ||
+      num_blocks < 0 || cache_slots < 0 || !(eps >= 0.f))
+    return NVK_EINVAL;
+  if (!(scale > 0.f)) return NVK_EINVAL;
+  if (dtype != NVK_DTYPE_BF16 || head_dim != nvk_qk::kHD) return NVK_EUNSUPPORTED;
+  if (num_q_heads % num_kv_heads) return NVK_EINVAL;
+  const int G = num_q_heads / num_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return NVK_EUNSUPPORTED;
+  if (batch == 0) return NVK_OK;
+  if (batch > kMaxBatch || num_kv_heads > 65535) return NVK_EUNSUPPORTED;
+  if (!qkv || !positions || !q_norm_weight || !k_norm_weight || !cos_sin_cache || !k_cache ||
+      !v_cache || !slot_mapping || !block_tables || !context_lens || !out)
+    return NVK_EINVAL;
+  if (bt_stride < max_blocks) return NVK_EINVAL;
+  if ((int64_t)block_size * max_blocks > INT32_MAX) return NVK_EINVAL;
+  if (max_position <= 0 || cos_sin_row_stride < head_dim) return NVK_EINVAL;
+  if (qkv_row_stride < ((int64_t)num_q_heads + 2 * num_kv_heads) * head_dim) return NVK_EINVAL;
+  const int tc = decode_tc(num_kv_heads, head_dim);
+  if ((int64_t)batch * num_kv_heads * (((int64_t)block_size * max_blocks + tc - 1) / tc) >
+      INT32_MAX)
+    return NVK_EINVAL;
+  if (((uintptr_t)qkv | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out |
+       (uintptr_t)q_norm_weight | (uintptr_t)k_norm_weight | (uintptr_t)cos_sin_cache) % 16)
+    return NVK_EALIGN;
+  if ((qkv_row_stride % 8) || (out_stride_tok % 8) || (out_stride_head % 8) ||
+      (cos_sin_row_stride % 4))
+    return NVK_EALIGN;
+  const size_t need =
+      decode_ws_bytes(batch, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks);
+  if (workspace == nullptr || workspace_bytes < need) return NVK_EWORKSPACE;
+  if ((uintptr_t)workspace % 256) return NVK_EALIGN;
+
+  DecodeArgs a = {};
+  a.q = nullptr;
+  a.k_cache = static_cast<const uint16_t*>(k_cache);
+  a.v_cache = static_cast<const uint16_t*>(v_cache);
+  a.block_tables = block_tables;
+  a.bt_stride = bt_stride;
+  a.context_lens = context_lens;
+  a.batch = batch;
+  a.num_q_heads = num_q_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.block_size = block_size;
+  a.bs_shift = nvk_log2_exact(block_size);
+  a.max_blocks = max_blocks;
+  a.num_blocks = num_blocks;
+  a.scale_log2 = scale * NVK_LOG2E;
+  a.out = static_cast<uint16_t*>(out);
+  a.out_stride_tok = out_stride_tok;
+  a.out_stride_head = out_stride_head;
+  a.hpi = decode_hpi(num_kv_heads, head_dim);
+  a.tc = tc;
+  a.n_waves = decode_waves(batch, num_kv_heads, head_dim, block_size, max_blocks);
+  const size_t desc = ((size_t)batch * (num_kv_heads / a.hpi) * 8 + 255) / 256 * 256;
+  a.ws_desc = static_cast<int32_t*>(workspace);
+  a.ws_rec = reinterpret_cast<float*>(static_cast<char*>(workspace) + desc);
+  a.qkv = static_cast<const uint16_t*>(qkv);
+  a.qkv_row_stride = qkv_row_stride;
+  a.positions = positions;
+  a.q_weight = static_cast<const uint16_t*>(q_norm_weight);
+  a.k_weight = static_cast<const uint16_t*>(k_norm_weight);
+  a.eps = eps;
+  a.cos_sin = cos_sin_cache;
+  a.cos_sin_stride = cos_sin_row_stride;
+  a.max_position = max_position;
+  a.slot_mapping = slot_mapping;
+  a.cache_slots = cache_slots;
+  a.k_store = static_cast<uint16_t*>(k_cache);
+  a.v_store = static_cast<uint16_t*>(v_cache);
+  const bool aligned = (block_size % tc) == 0;
+  return dispatch_group<128, true>(a, G, aligned, reinterpret_cast<hipStream_t>(stream));
 }

@@ -25,15 +25,13 @@
 // A workgroup owns one token (Hq + 2*Hkv rows, 8 KiB contiguous for Qwen3),
 // measured ~10 % faster than 16-row workgroups over the flattened row space,
 // which read the position, slot and cos/sin row once per row group.
-#include "nvk_common.h"
+#include "qk_math.h"
 
 namespace {
 
-constexpr int kHD = 128;
-constexpr int kLanesPerRow = kHD / 8;  // 16
+using nvk_qk::kHD;
+using nvk_qk::kLanesPerRow;
 constexpr int kMaxGroups = 32;  // row groups per workgroup (512 threads)
-
-#define NVK_DPP_ROW_ROR8 0x128
 
 struct PrologueArgs {
   const uint16_t* qkv;
@@ -70,9 +68,6 @@ __device__ __forceinline__ void store_nt(uint16_t* p, nvk_u32x4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<nvk_u32x4*>(p));
 }
 
-__device__ __forceinline__ float bf16_round(float x) {
-  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) << 16);
-}
 
 // One head row r of token t (uniform per 16-lane row group).
 __device__ __forceinline__ void prologue_row(const PrologueArgs& a, int64_t t, int r, int j,
@@ -92,52 +87,10 @@ __device__ __forceinline__ void prologue_row(const PrologueArgs& a, int64_t t, i
     return;
   }
 
-  float x[8];
-  const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[2 * i] = nvk_bf16lo_to_f32(w4[i]);
-    x[2 * i + 1] = nvk_bf16hi_to_f32(w4[i]);
-  }
-  // RMSNorm: var = mean(x^2) over the row (f32), x * rsqrt(var + eps) -> bf16,
-  // then times the bf16 weight -> bf16.
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-  ss = nvk_group_sum<kLanesPerRow>(ss);
-  const float rstd = rsqrtf(ss / (float)kHD + a.eps);
   const nvk_u32x4 wraw =
       *reinterpret_cast<const nvk_u32x4*>((is_q ? a.q_weight : a.k_weight) + 8 * j);
-  const uint32_t ww[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float n0 = bf16_round(x[2 * i] * rstd), n1 = bf16_round(x[2 * i + 1] * rstd);
-    x[2 * i] = bf16_round(n0 * nvk_bf16lo_to_f32(ww[i]));
-    x[2 * i + 1] = bf16_round(n1 * nvk_bf16hi_to_f32(ww[i]));
-  }
-  // Rotation: lanes 0-7 hold x1 (dims 0..63), lanes 8-15 x2 (dims 64..127);
-  // lane j's partner is lane j ^ 8 (a row rotation by 8 within 16 lanes).
-  const float* cs = a.cos_sin + pos * a.cos_sin_stride + 8 * (j & 7);
-  const nvk_f32x4 c0 = *reinterpret_cast<const nvk_f32x4*>(cs);
-  const nvk_f32x4 c1 = *reinterpret_cast<const nvk_f32x4*>(cs + 4);
-  const nvk_f32x4 s0 = *reinterpret_cast<const nvk_f32x4*>(cs + kHD / 2);
-  const nvk_f32x4 s1 = *reinterpret_cast<const nvk_f32x4*>(cs + kHD / 2 + 4);
-  const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-  const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-  const bool first_half = j < kLanesPerRow / 2;
-  float y[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float other = nvk_dpp<NVK_DPP_ROW_ROR8>(x[e]);
-    const float a0 = x[e] * cv[e];
-    const float a1 = other * sv[e];
-    y[e] = first_half ? a0 - a1 : a0 + a1;  // x1*cos - x2*sin | x2*cos + x1*sin
-  }
-  nvk_u32x4 outw;
-  outw.x = nvk_pack_bf16x2(y[0], y[1]);
-  outw.y = nvk_pack_bf16x2(y[2], y[3]);
-  outw.z = nvk_pack_bf16x2(y[4], y[5]);
-  outw.w = nvk_pack_bf16x2(y[6], y[7]);
+  const nvk_u32x4 outw =
+      nvk_qk::norm_rope8(raw, wraw, a.eps, a.cos_sin + pos * a.cos_sin_stride, j);
   if (is_q) {
     store_nt(a.q_out + t * a.q_out_stride_tok + (int64_t)r * a.q_out_stride_head + 8 * j, outw);
     return;

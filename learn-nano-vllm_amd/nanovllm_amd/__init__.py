@@ -13,9 +13,9 @@ from nanovllm_amd.layers.attention import Attention, store_kvcache
 from nanovllm_amd.flash_api import (flash_attn_varlen_func, flash_attn_with_kvcache,
                                     varlen_prefill, paged_decode)
 from nanovllm_amd.layers.prologue import (qk_norm_rope_store, attention_with_prologue,
-                                          rope_cos_sin_cache)
+                                          paged_decode_with_prologue, rope_cos_sin_cache)
 
 __all__ = ["Context", "get_context", "set_context", "reset_context", "Attention",
            "store_kvcache", "flash_attn_varlen_func", "flash_attn_with_kvcache",
            "varlen_prefill", "paged_decode", "qk_norm_rope_store", "attention_with_prologue",
-           "rope_cos_sin_cache"]
+           "paged_decode_with_prologue", "rope_cos_sin_cache"]

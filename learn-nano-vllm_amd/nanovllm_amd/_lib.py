@@ -50,6 +50,12 @@ SIGNATURES = {
                                               _c_i32, _c_i32, _c_ptr, _c_i64, _c_i64, _c_ptr,
                                               _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_i64,
                                               _c_i32, _c_ptr]),
+    "nvk_paged_decode_prologue": (ctypes.c_int, [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr,
+                                                 ctypes.c_float, _c_ptr, _c_i64, _c_i64, _c_ptr,
+                                                 _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr,
+                                                 _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                                 _c_i32, ctypes.c_float, _c_ptr, _c_i64, _c_i64,
+                                                 _c_ptr, ctypes.c_size_t, _c_i32, _c_ptr]),
     "nvk_prefill_metadata": (ctypes.c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i32, _c_i32, _c_i32,
                                             _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                                             _c_ptr]),

@@ -104,6 +104,25 @@ def test_error_codes_without_launching():
     assert lib.nvk_qk_norm_rope_store(*no_cache) == -1
     huge = list(pro); huge[2] = 1 << 31                                    # grid > 2^31 - 1
     assert lib.nvk_qk_norm_rope_store(*huge) == -1
+    # decode with the prologue: (qkv, stride, pos, qw, kw, eps, cos_sin, cs_stride, max_pos,
+    # k_cache, v_cache, slots, cache_slots, tables, bt_stride, lens, B, Hq, Hkv, D, bs,
+    # max_blocks, num_blocks, scale, out, out strides, ws, ws_bytes, dtype, stream)
+    dp = [16, 32 * 128, 16, 16, 16, 1e-6, 16, 128, 4096, 16, 16, 16, 1 << 20, 16, 8, 16, 4, 16, 8,
+          128, 256, 8, 1024, 0.088, 16, 16 * 128, 128, 16, 1 << 30, 0, None]
+    hd64 = list(dp); hd64[19] = 64
+    assert lib.nvk_paged_decode_prologue(*hd64) == -2                     # head_dim 64
+    fp16 = list(dp); fp16[29] = 1
+    assert lib.nvk_paged_decode_prologue(*fp16) == -2
+    none = list(dp); none[16] = 0
+    assert lib.nvk_paged_decode_prologue(*none) == 0                      # empty batch
+    no_slots = list(dp); no_slots[11] = None
+    assert lib.nvk_paged_decode_prologue(*no_slots) == -1
+    narrow = list(dp); narrow[1] = 31 * 128
+    assert lib.nvk_paged_decode_prologue(*narrow) == -1                   # row < Hq+2Hkv heads
+    mis = list(dp); mis[0] = 24
+    assert lib.nvk_paged_decode_prologue(*mis) == -3
+    small = list(dp); small[28] = 16
+    assert lib.nvk_paged_decode_prologue(*small) == -4                    # workspace too small
     # step metadata: (cached, new, offsets, ids, B, bs, width, T, cu_q, cu_k, pos, slots, tables)
     assert lib.nvk_prefill_metadata(16, 16, 16, 16, 9000, 256, 4, 10, 16, 16, 16, 16, 16,
                                     None) == -2                            # batch > 8192
