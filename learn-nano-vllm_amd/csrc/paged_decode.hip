@@ -557,26 +557,16 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 
 // Merges the partial records of groups cut between waves and writes the zero
 // output of empty contexts.  grid = (Hkv, B), block = G*HD threads.
-template <int HD, int G>
-__global__ __launch_bounds__(G * HD) void paged_decode_combine_kernel(DecodeArgs a) {
+// Merge of one output element over the parts of a cut group: wave p1's head
+// record (slot 0) and the continuation records (slot 1) of waves p1+1 .. p2
+// (every active wave's range holds at least kMinChunks chunks, so each of
+// them wrote one).  kBatch parts are fetched per round trip (3 kBatch loads
+// in flight), then folded into (M, L, O).  rec0: the record of wave 0, slot
+// 0, for this thread's kv head and q head.
+template <int kBatch, int HD, int G>
+__device__ __forceinline__ float merge_parts(const DecodeArgs& a, const float* rec0, int p1,
+                                             int p2, int d) {
   constexpr int REC_HEAD = G * (HD + 4);
-  const int kvh = blockIdx.x, b = blockIdx.y;
-  const int h = threadIdx.x / HD, d = threadIdx.x % HD;
-  const int n_blk = a.num_kv_heads / a.hpi;
-  const int hh = kvh % a.hpi;
-  const int2 desc = *reinterpret_cast<const int2*>(a.ws_desc + 2 * (b * n_blk + kvh / a.hpi));
-  uint16_t* op = a.out + (int64_t)b * a.out_stride_tok + (int64_t)(kvh * G + h) * a.out_stride_head + d;
-  if (desc.x < 0) {  // empty context (padded graph row): defined zero output
-    *op = 0;
-    return;
-  }
-  const int p1 = desc.x, p2 = desc.y;
-  if (p1 == p2) return;  // finished inside one wave
-  // Parts: wave p1's head record (slot 0) and the continuation records
-  // (slot 1) of waves p1+1 .. p2 (every active wave's range holds at least
-  // kMinChunks chunks, so each of them wrote one).  kBatch parts are fetched
-  // per round trip (48 loads in flight), then folded into (M, L, O).
-  constexpr int kBatch = 16;
   float M = -INFINITY, L = 0.f, O = 0.f;
   for (int base = p1; base <= p2; base += kBatch) {
     float mv[kBatch], lv[kBatch], ov[kBatch];
@@ -585,8 +575,7 @@ __global__ __launch_bounds__(G * HD) void paged_decode_combine_kernel(DecodeArgs
       const int p = base + u;
       const bool ok = p <= p2;
       const int pr = ok ? p : p1;
-      const float* rec = a.ws_rec + (((int64_t)pr * 2 + (pr == p1 ? 0 : 1)) * a.hpi + hh) * REC_HEAD +
-                         h * (HD + 4);
+      const float* rec = rec0 + ((int64_t)pr * 2 + (pr == p1 ? 0 : 1)) * a.hpi * REC_HEAD;
       mv[u] = rec[HD];
       lv[u] = rec[HD + 1];
       ov[u] = rec[d];
@@ -607,7 +596,30 @@ __global__ __launch_bounds__(G * HD) void paged_decode_combine_kernel(DecodeArgs
     }
     M = mb;
   }
-  *op = __builtin_bit_cast(uint16_t, (__bf16)(L > 0.f ? O / L : 0.f));
+  return L > 0.f ? O / L : 0.f;
+}
+
+template <int HD, int G>
+__global__ __launch_bounds__(G * HD) void paged_decode_combine_kernel(DecodeArgs a) {
+  constexpr int REC_HEAD = G * (HD + 4);  // floats per kv head in a record
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int h = threadIdx.x / HD, d = threadIdx.x % HD;
+  const int n_blk = a.num_kv_heads / a.hpi;
+  const int hh = kvh % a.hpi;
+  const int2 desc = *reinterpret_cast<const int2*>(a.ws_desc + 2 * (b * n_blk + kvh / a.hpi));
+  uint16_t* op = a.out + (int64_t)b * a.out_stride_tok + (int64_t)(kvh * G + h) * a.out_stride_head + d;
+  if (desc.x < 0) {  // empty context (padded graph row): defined zero output
+    *op = 0;
+    return;
+  }
+  const int p1 = desc.x, p2 = desc.y;
+  if (p1 == p2) return;  // finished inside one wave
+  const float* rec0 = a.ws_rec + hh * REC_HEAD + h * (HD + 4);
+  // groups cut into many parts (small batches, long contexts) fetch 32 per
+  // round trip; the others 16 (uniform over the workgroup)
+  const float r = p2 - p1 < 16 ? merge_parts<16, HD, G>(a, rec0, p1, p2, d)
+                               : merge_parts<32, HD, G>(a, rec0, p1, p2, d);
+  *op = __builtin_bit_cast(uint16_t, (__bf16)r);
 }
 
 // kv heads per load instruction.  One: a group is then one (sequence, kv
