@@ -432,25 +432,15 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
 // Merges the records of groups cut between waves and writes the zero rows of
 // groups with no key.  grid = (Hkv, batch), 512 threads: thread t owns row
 // t / 32 and d = 4 (t % 32) .. +3.
-__global__ __launch_bounds__(512) void short_query_combine_kernel(SqArgs a) {
-  const int kvh = blockIdx.x, s = blockIdx.y;
-  const int row = threadIdx.x >> 5, d0 = 4 * (threadIdx.x & 31);
-  const int Lq = seq_queries(a, s);
-  const int tok = row / a.G;
-  if (tok >= Lq) return;
-  const int head = kvh * a.G + row % a.G;
-  uint16_t* op = a.p.out + (int64_t)(a.p.cu_q[s] + tok) * a.p.out_stride_tok +
-                 (int64_t)head * a.p.out_stride_head + d0;
-  const int2 desc = *reinterpret_cast<const int2*>(a.desc + 2 * (s * a.p.num_kv_heads + kvh));
-  if (desc.x < 0) {
-    *reinterpret_cast<nvk_u32x2*>(op) = nvk_u32x2{0u, 0u};
-    return;
-  }
-  const int p1 = desc.x, p2 = desc.y;
-  if (p1 == p2) return;  // finished inside one wave
-  constexpr int kBatch = 8;
-  float M = -INFINITY, L = 0.f;
-  nvk_f32x4 O = {0.f, 0.f, 0.f, 0.f};
+// Merge of one row's 4 output columns over the parts p1..p2 of a cut group
+// (wave p1's head record, slot 0, then the continuation records, slot 1),
+// kBatch parts per round trip; returns the unnormalised sum O and its L.
+template <int kBatch>
+__device__ __forceinline__ void sq_merge_parts(const SqArgs& a, int row, int d0, int p1, int p2,
+                                               float& L, nvk_f32x4& O) {
+  float M = -INFINITY;
+  L = 0.f;
+  O = nvk_f32x4{0.f, 0.f, 0.f, 0.f};
   for (int base = p1; base <= p2; base += kBatch) {
     float mv[kBatch], lv[kBatch];
     nvk_f32x4 ov[kBatch];
@@ -479,6 +469,32 @@ __global__ __launch_bounds__(512) void short_query_combine_kernel(SqArgs a) {
     }
     M = mb;
   }
+}
+
+__global__ __launch_bounds__(512) void short_query_combine_kernel(SqArgs a) {
+  const int kvh = blockIdx.x, s = blockIdx.y;
+  const int row = threadIdx.x >> 5, d0 = 4 * (threadIdx.x & 31);
+  const int Lq = seq_queries(a, s);
+  const int tok = row / a.G;
+  if (tok >= Lq) return;
+  const int head = kvh * a.G + row % a.G;
+  uint16_t* op = a.p.out + (int64_t)(a.p.cu_q[s] + tok) * a.p.out_stride_tok +
+                 (int64_t)head * a.p.out_stride_head + d0;
+  const int2 desc = *reinterpret_cast<const int2*>(a.desc + 2 * (s * a.p.num_kv_heads + kvh));
+  if (desc.x < 0) {
+    *reinterpret_cast<nvk_u32x2*>(op) = nvk_u32x2{0u, 0u};
+    return;
+  }
+  const int p1 = desc.x, p2 = desc.y;
+  if (p1 == p2) return;  // finished inside one wave
+  // groups cut into more than 8 parts fetch 16 per round trip (uniform over
+  // the workgroup)
+  float L;
+  nvk_f32x4 O;
+  if (p2 - p1 < 8)
+    sq_merge_parts<8>(a, row, d0, p1, p2, L, O);
+  else
+    sq_merge_parts<16>(a, row, d0, p1, p2, L, O);
   const float inv = L > 0.f ? 1.f / L : 0.f;
   nvk_u32x2 wv;
   wv.x = nvk_pack_bf16x2(O[0] * inv, O[1] * inv);
