@@ -50,6 +50,14 @@ def test_decode_context_ladder_and_group_sizes(hq, hkv):
     _check(case, f"decode ladder G={hq // hkv}")
 
 
+def test_decode_groups_cut_into_many_parts():
+    """Two sequences over 1500 and 3000 keys: the stream-K split cuts each
+    (sequence, kv head) group into ~24 and ~47 wave parts, so the combine
+    takes its 32-record batch once and twice."""
+    case = decode_case(seed=11, ctx=[1500, 3000], pool_blocks=24)
+    _check(case, "decode groups of 24 and 47 parts")
+
+
 @pytest.mark.parametrize("bs", [16, 64, 512])
 def test_decode_other_block_sizes(bs):
     ctx = [1, 63, 64, 65, 700, 1500]
