@@ -173,7 +173,12 @@ size_t nvk_paged_decode_workspace_size(int32_t batch, int32_t num_q_heads,
  *   speculative-decode verification) the key range is split across
  *   workgroups whose partial results go to the workspace, and a second kernel
  *   merges them.  NULL (or too small) = no split; the result is the same up
- *   to rounding.  Two calls in flight at once need two workspaces.
+ *   to rounding.  Otherwise, for a multi-sequence prefill whose grid takes
+ *   more than two rounds of workgroups, a one-workgroup kernel first ranks
+ *   the (sequence, query tile) pairs by their key count into the workspace
+ *   and the attention kernel runs them longest first; without the workspace
+ *   they run in grid order, with the same output bits.  Two calls in flight
+ *   at once need two workspaces.
  * scale must be > 0.  dtype: NVK_DTYPE_BF16.  head_dim: 128.  G: 1, 2, 4 or 8.
  */
 int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,

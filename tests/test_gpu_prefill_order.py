@@ -1,0 +1,55 @@
+"""Longest-first query-tile order of the varlen prefill.  With a workspace
+(multi-sequence prefills) a small kernel ranks the (sequence, query tile)
+pairs by their key count and the attention kernel takes its tile from that
+order; without one the grid order is used.  The order only changes when a
+tile runs, so both calls must give the same bits, and the ordered one is also
+checked against the oracle (2e-2 abs / 1e-2 rel).  Cases: paged with cached
+prefixes (GQA groups 2, 4, 8; an empty sequence; one-token sequences) and
+dense self-attention."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_utils import assert_attn_close, oracle_prefill_dense, oracle_prefill_paged, say
+from test_gpu_prefill_split import _call, _paged_case
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (16, 4), (8, 1)])
+def test_ordered_equals_grid_order_paged(hq, hkv):
+    rng = np.random.default_rng(60 + hkv)
+    lens_q = [int(x) for x in rng.integers(1, 700, 24)] + [0, 1, 1] + [699]
+    lens_k = [q + int(c) for q, c in zip(lens_q, rng.integers(0, 600, len(lens_q)))]
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(61 + hkv, lens_q, lens_k, hq=hq, hkv=hkv)
+    args = (q.cuda(), kc.cuda(), vc.cuda(), cu_q.cuda(), cu_k.cuda(), max(lens_q), max(lens_k),
+            128 ** -0.5)
+    say(f"prefill order paged G={hq // hkv}: ordered")
+    ordered, ws = _call(*args, bt=bt.cuda(), use_ws=True)
+    tq = 128 * hkv // hq                      # query tokens per tile
+    pairs = len(lens_q) * ((max(lens_q) + tq - 1) // tq)
+    assert pairs * hkv > 1024 and ws >= 4 * pairs   # the order is used
+    say(f"prefill order paged G={hq // hkv}: grid order")
+    grid, _ = _call(*args, bt=bt.cuda(), use_ws=False)
+    assert torch.equal(ordered, grid)
+    ref = oracle_prefill_paged(q, kc, vc, bt, cu_q, cu_k, 256, 128 ** -0.5)
+    assert_attn_close(ordered, ref, f"ordered paged prefill G={hq // hkv}")
+
+
+def test_ordered_equals_grid_order_dense():
+    rng = np.random.default_rng(70)
+    lens = [int(x) for x in rng.integers(1, 500, 20)] + [499]   # 21 x 8 tiles x 8 heads
+    gen = torch.Generator().manual_seed(71)
+    t = sum(lens)
+    q = torch.randn(t, 16, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(t, 8, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(t, 8, 128, generator=gen).to(torch.bfloat16)
+    cu = torch.tensor([0] + np.cumsum(lens).tolist(), dtype=torch.int32)
+    args = (q.cuda(), k.cuda(), v.cuda(), cu.cuda(), cu.cuda(), max(lens), max(lens), 128 ** -0.5)
+    say("prefill order dense: ordered")
+    ordered, _ = _call(*args, use_ws=True)
+    say("prefill order dense: grid order")
+    grid, _ = _call(*args, use_ws=False)
+    assert torch.equal(ordered, grid)
+    assert_attn_close(ordered, oracle_prefill_dense(q, k, v, cu, cu, 128 ** -0.5),
+                      "ordered dense prefill")
