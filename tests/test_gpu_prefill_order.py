@@ -4,8 +4,8 @@ pairs by their key count and the attention kernel takes its tile from that
 order; without one the grid order is used.  The order only changes when a
 tile runs, so both calls must give the same bits, and the ordered one is also
 checked against the oracle (2e-2 abs / 1e-2 rel).  Cases: paged with cached
-prefixes (GQA groups 2, 4, 8; an empty sequence; one-token sequences) and
-dense self-attention."""
+prefixes (GQA groups 2, 4, 8; an empty sequence; one-token sequences),
+dense self-attention, and 300 short sequences (ties, empty sequences)."""
 import numpy as np
 import pytest
 import torch
@@ -53,3 +53,23 @@ def test_ordered_equals_grid_order_dense():
     assert torch.equal(ordered, grid)
     assert_attn_close(ordered, oracle_prefill_dense(q, k, v, cu, cu, 128 ** -0.5),
                       "ordered dense prefill")
+
+
+def test_ordered_many_short_sequences_with_empty_ones():
+    """300 sequences of 0-40 tokens (one query tile each, many ties and empty
+    sequences) over paged prefixes of 0-300 keys."""
+    rng = np.random.default_rng(80)
+    lens_q = [int(x) for x in rng.integers(0, 41, 300)]
+    lens_q[:3] = [0, 40, 1]
+    lens_k = [q + int(c) for q, c in zip(lens_q, rng.integers(0, 301, 300))]
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(81, lens_q, lens_k)
+    args = (q.cuda(), kc.cuda(), vc.cuda(), cu_q.cuda(), cu_k.cuda(), max(lens_q), max(lens_k),
+            128 ** -0.5)
+    say("prefill order, 300 short sequences: ordered")
+    ordered, ws = _call(*args, bt=bt.cuda(), use_ws=True)
+    assert ws >= 4 * 300
+    say("prefill order, 300 short sequences: grid order")
+    grid, _ = _call(*args, bt=bt.cuda(), use_ws=False)
+    assert torch.equal(ordered, grid)
+    ref = oracle_prefill_paged(q, kc, vc, bt, cu_q, cu_k, 256, 128 ** -0.5)
+    assert_attn_close(ordered, ref, "ordered prefill, 300 short sequences")
