@@ -155,7 +155,7 @@ def rotation(bytes_per_call, least=2):
 
 def host_threads(torch):
     """Host threads the CPU baseline runs on: the CPUs this process may use,
-    at most 16 (a one-GPU box's share)."""
+    at most 16 (the host cores that go with one GPU of an 8-GPU node)."""
     n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     torch.set_num_threads(max(1, min(16, n or 1)))
     return torch.get_num_threads()
