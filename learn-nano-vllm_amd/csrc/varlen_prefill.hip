@@ -93,10 +93,10 @@ constexpr int kRecFloats = HD + 4;  // partial record of one row: O[HD], m, l, p
 // first, is the longest-processing-time rule: the last workgroups to start
 // are short and the step ends with little idle time.  Measured on MI355X
 // (interleaved A/B, same process): 32 sequences of 512 cached + 100-1024 new
-// tokens 206 -> 188 us, 64 sequences of 256 + 16-512 128 -> 111 us, 16 of
-// 1024 + 256-2048 453 -> 363 us, 128 sequences of 16-400 tokens 138 -> 133
-// us; outputs bit-identical (every tile is computed the same way whatever
-// runs when).  One workgroup counting-sorts the pairs by cost (ties in any
+// tokens 206 -> 194 us, 64 sequences of 256 + 16-512 130 -> 117 us, 16 of
+// 1024 + 256-2048 452 -> 375 us, 128 sequences of 16-400 tokens 141 -> 139
+// us, this kernel included; outputs bit-identical (every tile is computed
+// the same way whatever runs when).  One workgroup counting-sorts the pairs by cost (ties in any
 // order: any permutation of the pairs gives the same output).
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderBuckets = 4096;      // costs above kOrderBuckets - 1 share the last
