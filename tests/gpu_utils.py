@@ -62,6 +62,16 @@ def oracle_decode(q, k_cache, v_cache, block_tables, context_lens, block_size, s
                                block_size=block_size)
 
 
+def oracle_paged_bits(q, k_cache, v_cache, block_tables, cu_q, lens_k, block_size, scale):
+    """Oracle over bf16 tensors passed as bit patterns, so that only the rows a
+    sequence reads are widened (large caches); any device."""
+    return orc.paged_attention(bits(q), bits(k_cache), bits(v_cache),
+                               np.asarray(cu_q.cpu() if hasattr(cu_q, "cpu") else cu_q),
+                               np.asarray(lens_k.cpu() if hasattr(lens_k, "cpu") else lens_k),
+                               scale, block_tables=block_tables.cpu().numpy(),
+                               block_size=block_size)
+
+
 def oracle_prefill_paged(q, k_cache, v_cache, block_tables, cu_q, cu_k, block_size, scale):
     lens_k = np.diff(cu_k.numpy())
     return orc.paged_attention(f32(q), f32(k_cache), f32(v_cache), cu_q.numpy(), lens_k, scale,

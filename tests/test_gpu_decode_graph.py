@@ -86,3 +86,64 @@ def test_bucketed_decode_graph_replays_match_oracle():
         runner.run(torch.zeros(MAX_BS + 1, dtype=torch.int64, device=dev),
                    qkv=torch.zeros(MAX_BS + 1, L, (HQ + 2 * HKV) * D, dtype=torch.bfloat16,
                                    device=dev))
+
+
+@pytest.mark.gpu
+def test_large_buckets_replay_live_batches_below_their_bucket():
+    """Buckets 48..512 of the reference's list (model_runner.py:234) with live
+    batches of 33, 40, 100, 250 and 500 sequences (padded rows in every
+    replay, a smaller batch after a larger one leaves stale table rows and
+    columns) over contexts U{1..4096} (max_model_len, config.py:11).  Pages
+    before a sequence's last one come from 64 pages shared read-only across
+    sequences; the last page, where the new token is stored, is private."""
+    nb, w, max_bs = 64 + 512, 16, 512
+    say("decode graph, large buckets: capture 1..512")
+    dev = torch.device("cuda:0")
+    layers, rope, kv_cache, step = decode_stack(L, nb, dev, seed=33)
+    runner = DecodeGraphRunner(step, max_bs, w, inputs={"qkv": ((L, (HQ + 2 * HKV) * D),
+                                                                torch.bfloat16)},
+                               output=((L, HQ * D), torch.bfloat16), device=dev)
+    assert runner.buckets[:7] == [1, 2, 4, 8, 16, 32, 48] and runner.buckets[-1] == 512
+    cos_sin = rope.cos_sin_cache.reshape(-1, D).cpu().numpy()
+    rng = np.random.default_rng(34)
+    gen = torch.Generator().manual_seed(35)
+    for rep, live in enumerate([500, 40, 250, 33, 100]):
+        lens = rng.integers(1, 4097, live).astype(np.int32)
+        private = rng.permutation(512)[:live] + 64
+        bt = np.full((live, w), -1, np.int32)
+        for i, n in enumerate(lens):
+            need = -(-int(n) // BS)
+            bt[i, :need - 1] = rng.choice(64, need - 1, replace=False)
+            bt[i, need - 1] = private[i]
+        slots = (private * BS + (lens - 1) % BS).astype(np.int32)
+        pos = torch.from_numpy(lens.astype(np.int64) - 1)
+        qkv = (torch.randn(live, L, (HQ + 2 * HKV) * D, generator=gen) * 2.0).to(torch.bfloat16)
+        before = bits(kv_cache).copy()
+        say(f"decode graph replay {rep}: live={live} bucket={runner.bucket(live)}")
+        set_context(False, slot_mapping=torch.from_numpy(slots).to(dev),
+                    context_lens=torch.from_numpy(lens).to(dev),
+                    block_tables=torch.from_numpy(bt).to(dev))
+        try:
+            out = runner.run(pos.to(dev), qkv=qkv.to(dev)).clone()
+            padded = runner.outputs[live:runner.bucket(live)].clone()
+            torch.cuda.synchronize()
+        finally:
+            reset_context()
+        assert padded.eq(0).all(), "padded rows must be zero"
+        after = bits(kv_cache)
+        sl = slots.astype(np.int64)
+        for i, (attn, qn, kn) in enumerate(layers):
+            kc_ref, vc_ref = before[0, i].copy(), before[1, i].copy()
+            q_ref, k_ref, _ = orc.qk_norm_rope_store(
+                bits(qkv[:, i]), pos.numpy(), bits(qn.weight), bits(kn.weight), qn.eps, cos_sin,
+                HQ, HKV, D, kc_ref, vc_ref, sl)
+            assert np.array_equal(after[1, i], vc_ref), f"replay {rep} layer {i}: v cache"
+            kc_got = after[0, i].reshape(nb * BS, HKV, D)
+            untouched = np.ones(nb * BS, dtype=bool)
+            untouched[sl] = False
+            assert np.array_equal(kc_got[untouched],
+                                  before[0, i].reshape(nb * BS, HKV, D)[untouched])
+            assert_rotated_close(kc_got[sl], k_ref, f"replay {rep} layer {i}: cached k")
+            ref = orc.paged_attention(q_ref, after[0, i], after[1, i], np.arange(live + 1), lens,
+                                      D ** -0.5, block_tables=bt, block_size=BS)
+            assert_attn_close(out[:, i].reshape(live, HQ, D), ref, f"replay {rep} layer {i}")
