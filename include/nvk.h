@@ -56,6 +56,7 @@ extern "C" {
 #define NVK_EUNSUPPORTED (-2) /* head_dim / group size / dtype not built          */
 #define NVK_EALIGN (-3)       /* pointer or stride misaligned for the element type */
 #define NVK_EWORKSPACE (-4)   /* workspace missing or smaller than required       */
+#define NVK_ESCRATCH (-5)     /* sizes exceed the no-allocation entry's scratch    */
 
 /* element types of q / k / v / caches / outputs */
 #define NVK_DTYPE_BF16 0
@@ -139,6 +140,35 @@ int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
 size_t nvk_paged_decode_workspace_size(int32_t batch, int32_t num_q_heads,
                                        int32_t num_kv_heads, int32_t head_dim,
                                        int32_t block_size, int32_t max_blocks);
+
+/*
+ * nvk_paged_decode without a workspace argument: it allocates nothing.
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture that may not call hipMalloc, serving
+ * loops and harnesses that forbid allocation.
+ *
+ * Same arguments, kernels and results (bit for bit) as nvk_paged_decode; the
+ * workspace is instead a static device array of NVK_NOALLOC_SCRATCH_BYTES
+ * inside the library, one per GPU, held until the process ends.  Sizes whose
+ * nvk_paged_decode_workspace_size() exceeds it are rejected with
+ * NVK_ESCRATCH before anything is launched (Qwen3-0.6B shapes need at most
+ * 4.5 MB at batch 2048; group size 8 at most 17.5 MB).  The scratch of the
+ * current device is used (looked up once per device), and `stream` must
+ * belong to that device (else NVK_EINVAL).  Every call on one GPU shares its
+ * scratch: two calls that overlap on one GPU (different streams, or two host
+ * threads) race and give undefined results; calls ordered on one stream are
+ * safe.  Nothing in the scratch needs clearing between calls.
+ */
+#define NVK_NOALLOC_SCRATCH_BYTES (20u << 20)
+int nvk_paged_decode_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                             const void* k_cache, const void* v_cache,
+                             const int32_t* block_tables, int64_t bt_stride,
+                             const int32_t* context_lens,
+                             int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t block_size, int32_t max_blocks,
+                             int32_t num_blocks, float scale,
+                             void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                             int32_t dtype, void* stream);
 
 /*
  * Varlen causal attention over new tokens, with or without a paged prefix.

@@ -168,6 +168,9 @@ extern "C" const char* nvk_strerror(int code) {
     case NVK_EUNSUPPORTED: return "nvk: unsupported head_dim / group size / dtype";
     case NVK_EALIGN: return "nvk: pointer or stride misaligned for the element type";
     case NVK_EWORKSPACE: return "nvk: workspace missing or too small";
+    case NVK_ESCRATCH:
+      return "nvk: these sizes need more than the static scratch of the no-allocation entry "
+             "point (NVK_NOALLOC_SCRATCH_BYTES); use the entry point with a workspace";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

@@ -42,6 +42,8 @@
 // merges the cut groups after two dependent reads and writes the zero rows of
 // empty contexts.  (Merging inside the main kernel needs cross-XCD release /
 // acquire fences per part; on MI355X those cost far more than the combine.)
+#include <mutex>
+
 #include "nvk_common.h"
 #include "qk_math.h"
 
@@ -683,25 +685,16 @@ int dispatch_group(const DecodeArgs& a, int G, bool aligned, hipStream_t s) {
   }
 }
 
-}  // namespace
-
-extern "C" size_t nvk_paged_decode_workspace_size(int32_t batch, int32_t num_q_heads,
-                                                  int32_t num_kv_heads, int32_t head_dim,
-                                                  int32_t block_size, int32_t max_blocks) {
-  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 ||
-      max_blocks <= 0 || num_q_heads % num_kv_heads || (head_dim != 64 && head_dim != 128))
-    return 0;
-  return decode_ws_bytes(batch, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks);
-}
-
-extern "C" int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
-                                const void* k_cache, const void* v_cache,
-                                const int32_t* block_tables, int64_t bt_stride,
-                                const int32_t* context_lens, int32_t batch, int32_t num_q_heads,
-                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                int32_t max_blocks, int32_t num_blocks, float scale, void* out,
-                                int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
-                                size_t workspace_bytes, int32_t dtype, void* stream) {
+// Checks the arguments of a plain decode call (everything but the workspace)
+// and fills `a`; returns NVK_OK, or the error code, before anything is
+// launched.  *need = workspace bytes the call uses.
+int decode_setup(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                 const void* v_cache, const int32_t* block_tables, int64_t bt_stride,
+                 const int32_t* context_lens, int32_t batch, int32_t num_q_heads,
+                 int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t max_blocks,
+                 int32_t num_blocks, float scale, void* out, int64_t out_stride_tok,
+                 int64_t out_stride_head, int32_t dtype, DecodeArgs& a, size_t* need) {
+  *need = 0;
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 || max_blocks <= 0 ||
       num_blocks < 0)
     return NVK_EINVAL;
@@ -726,12 +719,9 @@ extern "C" int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_s
     return NVK_EALIGN;
   if ((q_stride_tok % 8) || (q_stride_head % 8) || (out_stride_tok % 8) || (out_stride_head % 8))
     return NVK_EALIGN;
-  const size_t need =
-      decode_ws_bytes(batch, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks);
-  if (workspace == nullptr || workspace_bytes < need) return NVK_EWORKSPACE;
-  if ((uintptr_t)workspace % 256) return NVK_EALIGN;
+  *need = decode_ws_bytes(batch, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks);
 
-  DecodeArgs a = {};
+  a = DecodeArgs{};
   a.q = static_cast<const uint16_t*>(q);
   a.q_stride_tok = q_stride_tok;
   a.q_stride_head = q_stride_head;
@@ -754,13 +744,112 @@ extern "C" int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_s
   a.hpi = decode_hpi(num_kv_heads, head_dim);
   a.tc = tc;
   a.n_waves = decode_waves(batch, num_kv_heads, head_dim, block_size, max_blocks);
-  const size_t desc = ((size_t)batch * (num_kv_heads / a.hpi) * 8 + 255) / 256 * 256;
+  return NVK_OK;
+}
+
+// Points the descriptors and records of `a` into `workspace` and launches.
+int decode_run(DecodeArgs& a, int head_dim, void* workspace, hipStream_t s) {
+  const size_t desc = ((size_t)a.batch * (a.num_kv_heads / a.hpi) * 8 + 255) / 256 * 256;
   a.ws_desc = static_cast<int32_t*>(workspace);
   a.ws_rec = reinterpret_cast<float*>(static_cast<char*>(workspace) + desc);
-  const bool aligned = (block_size % tc) == 0;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool aligned = (a.block_size % a.tc) == 0;
+  const int G = a.num_q_heads / a.num_kv_heads;
   if (head_dim == 128) return dispatch_group<128>(a, G, aligned, s);
   return dispatch_group<64>(a, G, aligned, s);
+}
+
+// Scratch of nvk_paged_decode_noalloc: one copy per GPU (the code object's
+// device globals are instantiated on every device it is loaded on), held
+// until the process ends.  Host code must not use the name `scratch` as a
+// device address: its per-device address comes from hipGetSymbolAddress.
+constexpr size_t kScratchBytes = NVK_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of this GPU's scratch, looked up once per device with that
+// device current (the device `stream` belongs to must be the current one).
+int scratch_for_stream(hipStream_t stream, void** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (stream != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return (int)e;
+    if (sdev != dev) return NVK_EINVAL;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return NVK_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr || (uintptr_t)p % 256) return NVK_EALIGN;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return NVK_OK;
+}
+
+}  // namespace
+
+extern "C" size_t nvk_paged_decode_workspace_size(int32_t batch, int32_t num_q_heads,
+                                                  int32_t num_kv_heads, int32_t head_dim,
+                                                  int32_t block_size, int32_t max_blocks) {
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 ||
+      max_blocks <= 0 || num_q_heads % num_kv_heads || (head_dim != 64 && head_dim != 128))
+    return 0;
+  return decode_ws_bytes(batch, num_q_heads, num_kv_heads, head_dim, block_size, max_blocks);
+}
+
+extern "C" int nvk_paged_decode(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                const void* k_cache, const void* v_cache,
+                                const int32_t* block_tables, int64_t bt_stride,
+                                const int32_t* context_lens, int32_t batch, int32_t num_q_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                int32_t max_blocks, int32_t num_blocks, float scale, void* out,
+                                int64_t out_stride_tok, int64_t out_stride_head, void* workspace,
+                                size_t workspace_bytes, int32_t dtype, void* stream) {
+  DecodeArgs a;
+  size_t need = 0;
+  const int st = decode_setup(q, q_stride_tok, q_stride_head, k_cache, v_cache, block_tables,
+                              bt_stride, context_lens, batch, num_q_heads, num_kv_heads,
+                              head_dim, block_size, max_blocks, num_blocks, scale, out,
+                              out_stride_tok, out_stride_head, dtype, a, &need);
+  if (st != NVK_OK || batch == 0) return st;
+  if (workspace == nullptr || workspace_bytes < need) return NVK_EWORKSPACE;
+  if ((uintptr_t)workspace % 256) return NVK_EALIGN;
+  return decode_run(a, head_dim, workspace, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int nvk_paged_decode_noalloc(const void* q, int64_t q_stride_tok,
+                                        int64_t q_stride_head, const void* k_cache,
+                                        const void* v_cache, const int32_t* block_tables,
+                                        int64_t bt_stride, const int32_t* context_lens,
+                                        int32_t batch, int32_t num_q_heads,
+                                        int32_t num_kv_heads, int32_t head_dim,
+                                        int32_t block_size, int32_t max_blocks,
+                                        int32_t num_blocks, float scale, void* out,
+                                        int64_t out_stride_tok, int64_t out_stride_head,
+                                        int32_t dtype, void* stream) {
+  DecodeArgs a;
+  size_t need = 0;
+  const int st = decode_setup(q, q_stride_tok, q_stride_head, k_cache, v_cache, block_tables,
+                              bt_stride, context_lens, batch, num_q_heads, num_kv_heads,
+                              head_dim, block_size, max_blocks, num_blocks, scale, out,
+                              out_stride_tok, out_stride_head, dtype, a, &need);
+  if (st != NVK_OK || batch == 0) return st;
+  if (need > kScratchBytes) return NVK_ESCRATCH;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  const int sst = scratch_for_stream(s, &ws);
+  if (sst != NVK_OK) return sst;
+  // Every descriptor and record the kernels read is written earlier in the
+  // same call, so the scratch needs no clearing between calls.
+  return decode_run(a, head_dim, ws, s);
 }
 
 extern "C" int nvk_paged_decode_prologue(

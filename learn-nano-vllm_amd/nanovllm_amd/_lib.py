@@ -38,6 +38,10 @@ SIGNATURES = {
                                         ctypes.c_size_t, _c_i32, _c_ptr]),
     "nvk_paged_decode_workspace_size": (ctypes.c_size_t,
                                         [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "nvk_paged_decode_noalloc": (ctypes.c_int, [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr,
+                                                _c_i64, _c_ptr, _c_i32, _c_i32, _c_i32, _c_i32,
+                                                _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_ptr,
+                                                _c_i64, _c_i64, _c_i32, _c_ptr]),
     "nvk_varlen_prefill": (ctypes.c_int, [_c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i64,
                                           _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i32, _c_i32,
                                           _c_i32, _c_ptr, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,

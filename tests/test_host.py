@@ -67,6 +67,14 @@ def test_error_codes_without_launching():
     # tiny problem: one wave per chunk (B=1, 1 kv head, 64-token table: 2 chunks -> 1 WG)
     assert lib.nvk_paged_decode_workspace_size(1, 2, 1, 128, 64, 1) == 256 + 4 * 2 * 2 * 132 * 4
     assert lib.nvk_paged_decode_workspace_size(4, 16, 5, 128, 256, 1) == 0   # 16 % 5 != 0
+    # the no-allocation decode: the same argument checks, and sizes whose
+    # workspace exceeds its 20 MiB static scratch rejected before any launch
+    assert lib.nvk_strerror(-5).startswith(b"nvk:")
+    assert lib.nvk_paged_decode_noalloc(*args[:19], 1, None) == -2          # fp16
+    assert lib.nvk_paged_decode_noalloc(*bad_scale[:19], 0, None) == -1
+    huge = list(args); huge[8], huge[9], huge[10] = 2048, 8192, 1024
+    assert lib.nvk_paged_decode_workspace_size(2048, 8192, 1024, 128, 256, 8) > 20 << 20
+    assert lib.nvk_paged_decode_noalloc(*huge[:19], 0, None) == -5
     # prefill: head_dim 64 not built
     assert lib.nvk_varlen_prefill(16, 2048, 128, 4, 16, 16, 1024, 1024, 128, 4, 16, 16, 1, 4, 4,
                                   None, 0, 0, 0, 0, 16, 8, 64, 0.1, 16, 2048, 128, None, 0, 0,
