@@ -26,13 +26,24 @@ peak).
 Timing: each leg builds K steps into one HIP graph cycling over copies of its
 inputs (as many as make one cycle touch >= 1 GiB, 4x the 256 MB Infinity
 Cache, so no step finds its working set cached from the previous use of its
-copy), replays a W-step graph first as warmup, then
-brackets one replay of the K-step graph with device synchronisation (wall
-clock -> ms_per_step) and HIP events on the launch stream (-> roofline
-achieved).  The CPU baseline of the store, decode and prefill legs is the
-reference's path on the host CPU in PyTorch (index_put, block-table gather +
-scaled_dot_product_attention; oracle/torch_cpu.py) on up to 16 host threads;
-the prologue's is the numpy oracle on one thread.  Both run on the same inputs.
+copy), replays a W-step graph as warmup and keeps replaying it until at
+least 50 ms of warm replays have run (so the clocks are up whatever W is),
+then brackets one replay of the K-step graph with device synchronisation
+(wall clock -> ms_per_step) and HIP events on the launch stream (-> roofline
+achieved).  Beside the store, a device copy of the same bytes (and one of 512
+MiB) under the same rotation gives the copy rate this box reaches.
+
+CPU baselines run after every GPU leg: the reference's path on the host CPU
+in PyTorch (oracle/torch_cpu.py: index_put for the store, block-table gather +
+scaled_dot_product_attention for decode, prefill, spec-verify and the mixed
+step, the eager RMSNorm / rotary / store tensor operations for the prologue)
+on up to 16 host threads, on the same inputs (the mixed step on one layer,
+scaled by 28).
+
+roofline.traffic (HBM bytes per step behind the L2) comes from
+profiles/hbm_traffic.json, written by --collect-traffic from rocprofv3
+FETCH_SIZE / WRITE_SIZE runs; it is reported only when the file was measured
+on the kernel sources being timed (a hash of csrc/ and include/), else null.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                   [--legs decode,store,prologue,prefill,spec,graph,metadata,sampler,mixed]
@@ -43,10 +54,16 @@ counter collection with rocprofv3, which profiles individual dispatches).
 --copy-calibration MiB only runs a plain device-to-device copy of that size
 (5 launches) and exits: the reference kernel of known traffic against which
 the HBM counters (FETCH_SIZE / WRITE_SIZE) of the legs are scaled.
+--collect-traffic DIR OUT reads the counter runs under DIR (named
+<COUNTER>_copy and <COUNTER>_<leg>, see profiles/hbm_traffic_counters.md) and
+writes the traffic file OUT.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
+import hashlib
 import json
 import os
 import statistics
@@ -76,6 +93,8 @@ def parse_args():
                    help="launch steps one by one (no graph), e.g. under rocprofv3 --pmc")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MiB",
                    help="only run a plain device copy of MiB mebibytes (counter calibration)")
+    p.add_argument("--collect-traffic", nargs=2, metavar=("DIR", "OUT"),
+                   help="write the traffic file OUT from the rocprofv3 counter runs under DIR")
     return p.parse_args()
 
 
@@ -83,11 +102,19 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+MIN_WARM_S = 0.05   # every leg warms for at least this long before its timed replay
+
+
 def time_eager(torch, step_fns, steps, warmup):
     """Launch `steps` calls (cycling over step_fns) one by one; return
     (wall seconds per step, event seconds per step)."""
-    for i in range(max(1, warmup)):
+    t_warm = time.perf_counter()
+    i = 0
+    while i < max(1, warmup) or time.perf_counter() - t_warm < MIN_WARM_S:
         step_fns[i % len(step_fns)]()
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -101,7 +128,8 @@ def time_eager(torch, step_fns, steps, warmup):
 
 def time_graph(torch, step_fns, steps, warmup, eager=False):
     """Capture `steps` calls (cycling over step_fns) in one graph; return
-    (wall seconds per step, event seconds per step)."""
+    (wall seconds per step, event seconds per step).  The warmup graph of
+    `warmup` steps is replayed until at least MIN_WARM_S of replays ran."""
     if eager:
         return time_eager(torch, step_fns, steps, warmup)
     def capture(n, start):
@@ -120,10 +148,15 @@ def time_graph(torch, step_fns, steps, warmup, eager=False):
     # the timed steps continue the cycle where the warmup stopped
     g_warm = capture(max(1, warmup), 0)
     g = capture(steps, max(1, warmup) % len(step_fns))
+    torch.cuda.synchronize()
+    t_warm = time.perf_counter()
     g_warm.replay()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    one = max(time.perf_counter() - t_warm, 1e-6)
+    for _ in range(int((MIN_WARM_S - one) / one) + 1 if one < MIN_WARM_S else 0):
+        g_warm.replay()
     torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
     g.replay()
@@ -161,15 +194,110 @@ def host_threads(torch):
     return torch.get_num_threads()
 
 
+def kernel_source_hash():
+    """sha256 over the kernel sources (learn-nano-vllm_amd/csrc/*, include/*.h):
+    the traffic file is valid only for the sources it was measured on."""
+    h = hashlib.sha256()
+    files = sorted(glob.glob(os.path.join(ROOT, "learn-nano-vllm_amd", "csrc", "*")) +
+                   glob.glob(os.path.join(ROOT, "include", "*.h")))
+    for f in files:
+        h.update(os.path.relpath(f, ROOT).encode())
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
+
+
 def traffic_for(leg):
+    """HBM bytes per step of a leg, or None when the traffic file is missing or
+    was measured on other kernel sources than the ones built here."""
     try:
         with open(TRAFFIC_FILE) as f:
-            return json.load(f).get(leg, {}).get("bytes_per_launch")
+            data = json.load(f)
     except (OSError, ValueError):
         return None
+    if data.get("source_sha256") != kernel_source_hash():
+        return None
+    return data.get("legs", {}).get(leg, {}).get("bytes_per_launch")
 
 
-def mixed_leg(torch, dev, args, orc, layers=28):
+# Traffic collection: per leg, the bench run that holds it (--legs), the
+# kernels of one step, and the kernel launched once per step.
+TRAFFIC_LEGS = {
+    "decode": ("decode", ("paged_decode_kernel", "paged_decode_combine_kernel"),
+               "paged_decode_kernel"),
+    "kv_store": ("store", ("kv_store_rows_kernel",), "kv_store_rows_kernel"),
+    "prologue": ("prologue", ("qk_prologue_kernel",), "qk_prologue_kernel"),
+    "prefill": ("prefill", ("varlen_prefill_kernel", "prefill_tile_order_kernel"),
+                "varlen_prefill_kernel"),
+    "spec_verify": ("spec", ("short_query_kernel", "short_query_combine_kernel"),
+                    "short_query_kernel"),
+}
+
+
+def _base_name(kernel_name):
+    """'void (anonymous namespace)::foo<1, 2>((anonymous namespace)::Args)' -> 'foo'."""
+    head = kernel_name.replace("(anonymous namespace)::", "")
+    head = head[5:] if head.startswith("void ") else head
+    for sep in ("<", "("):
+        head = head.split(sep)[0]
+    return head.strip()
+
+
+def _counter_rows(run_dir):
+    files = glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {run_dir}")
+    rows = []
+    for f in files:
+        with open(f) as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def collect_traffic(run_root, out_path):
+    """Per leg, mean HBM bytes per step from the FETCH_SIZE and WRITE_SIZE runs,
+    each counter scaled by what it reads for the 512 MiB calibration copy."""
+    scale = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        vals = [float(r["Counter_Value"]) for r in _counter_rows(f"{run_root}/{counter}_copy")
+                if r["Counter_Name"] == counter and "copyBuffer" in r["Kernel_Name"]]
+        if not vals:
+            raise SystemExit(f"{counter}: no copy dispatch in the calibration run")
+        scale[counter] = (512 << 20) / (statistics.mean(vals) * 1024.0)
+    legs = {}
+    for leg, (run, kernels, main_kernel) in TRAFFIC_LEGS.items():
+        per = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            sums, counts = {}, {}
+            for r in _counter_rows(f"{run_root}/{counter}_{run}"):
+                name = r["Kernel_Name"]
+                if r["Counter_Name"] != counter or _base_name(name) not in kernels:
+                    continue
+                sums[name] = sums.get(name, 0.0) + float(r["Counter_Value"])
+                counts[name] = counts.get(name, 0) + 1
+            steps = sum(c for n, c in counts.items() if _base_name(n) == main_kernel)
+            if not steps:
+                raise SystemExit(f"{leg}: no {main_kernel} dispatch in {counter}_{run}")
+            for name in sums:
+                per.setdefault(name, {"dispatches": counts[name]})
+                key = "read_bytes" if counter == "FETCH_SIZE" else "write_bytes"
+                per[name][key] = int(sums[name] * 1024.0 * scale[counter] / steps)
+        rd = sum(k.get("read_bytes", 0) for k in per.values())
+        wr = sum(k.get("write_bytes", 0) for k in per.values())
+        legs[leg] = {"bytes_per_launch": rd + wr, "read_bytes": rd, "write_bytes": wr,
+                     "kernels": per}
+    data = {"_note": "HBM-side bytes per step (every kernel of the operator, per eager step), "
+                     "from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of bench.py --eager, "
+                     "each scaled by what the counter reads for a 512 MiB device copy",
+            "source_sha256": kernel_source_hash(),
+            "scale": {k: round(v, 4) for k, v in scale.items()},
+            "legs": legs}
+    with open(out_path, "w") as f:
+        json.dump(data, f, indent=1)
+    print(json.dumps({k: v["bytes_per_launch"] for k, v in legs.items()}), flush=True)
+
+
+def mixed_leg(torch, dev, args, orc, cpu_jobs, layers=28):
     """28 layers of one mixed step, each with its own KV pool (random bf16 made on
     the GPU) and the same block tables / slots; a layer = KV-store of every new
     token, the prefill chunks, the decodes."""
@@ -214,6 +342,8 @@ def mixed_leg(torch, dev, args, orc, layers=28):
     t_roof = layers * ((dec_bytes + st_bytes) / (HBM_PEAK_GBS * 1e9) +
                        pf_flops / (BF16_PEAK_TFLOPS * 1e12))
     del pools
+    if not args.no_cpu_baseline:
+        cpu_jobs.append(("mixed_step", lambda: mixed_cpu_baseline(torch, layers)))
     return dict(ms_per_step=wall * 1e3, layers=layers, steps=steps,
                 workload="28 layers x (KV-store 4288 tokens + 8 prefill chunks of 512 after "
                          "U{0..1536} cached + 192 decodes over U{256..4096}), 3300-page pool "
@@ -225,14 +355,41 @@ def mixed_leg(torch, dev, args, orc, layers=28):
                           "frac": round(t_roof / ev, 4)})
 
 
-def prologue_leg(torch, dev, args, orc, bits):
+def mixed_cpu_baseline(torch, layers):
+    """One layer of the mixed step through the PyTorch CPU path (index_put store
+    of the 4288 new tokens, then gather + SDPA attention of the 8 prefill
+    chunks and of the 192 decodes) on the same metadata, scaled by the layers
+    of the step."""
+    from oracle import torch_cpu as tcpu
+    from nanovllm_amd.workloads import mixed_layer_case
+
+    threads = host_threads(torch)
+    log(f"cpu baseline: one mixed-step layer on the PyTorch CPU path, {threads} threads")
+    mc = mixed_layer_case()
+    kc, vc = mc.k_cache, mc.v_cache
+
+    def layer():
+        tcpu.store_kvcache_cpu(mc.key, mc.value, kc, vc, mc.slot_mapping)
+        tcpu.paged_attention_cpu(mc.q_prefill, kc, vc, mc.cu_seqlens_q, mc.lens_k, mc.scale,
+                                 mc.prefill_block_tables)
+        tcpu.paged_attention_cpu(mc.q_decode, kc, vc, range(len(mc.dec_lens) + 1),
+                                 mc.context_lens, mc.scale, mc.decode_block_tables)
+
+    t = cpu_time(layer, 3)
+    return {"value": round(t * layers * 1e3, 2), "unit": "ms/step", "cores": threads,
+            "kind": "port",
+            "sample": f"one of the {layers} layers (store of 4288 tokens, 8 prefill chunks of 512, "
+                      "192 decodes) through the PyTorch CPU path, median of 3 reps on "
+                      f"{threads} host threads (os.cpu_count() = {os.cpu_count()}), times "
+                      f"{layers}"}
+
+
+def prologue_leg(torch, dev, args, orc, cpu_jobs):
     """Fused q/k RMSNorm + RoPE + KV-store over the mixed step's 4288 new tokens
     of one layer (rotated copies of the inputs storing into one 3300-page pool), and the
     same steps as separate eager torch operations (the reference's
     layernorm.py:16-26 / rotary_embedding.py:6-14 code, then the store) for
     comparison."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
     from nanovllm_amd import qk_norm_rope_store, store_kvcache
     from nanovllm_amd.workloads import prologue_case
 
@@ -293,19 +450,23 @@ def prologue_leg(torch, dev, args, orc, bits):
                          "frac": round(pbytes / ev / 1e9 / HBM_PEAK_GBS, 4),
                          "traffic": traffic_for("prologue")})
     if not args.no_cpu_baseline:
-        qkv_b, pos = bits(pc.qkv), pc.positions.numpy()
-        qw, kw, cs = bits(pc.q_weight), bits(pc.k_weight), pc.cos_sin.reshape(-1, hd).numpy()
-        sl = pc.slot_mapping.numpy()
-        kc_h = np.zeros((pc.pool_blocks, pc.block_size, hkv, hd), dtype=np.uint16)
-        vc_h = np.zeros_like(kc_h)
-        with threadpool_limits(1):
-            t = cpu_time(lambda: orc.qk_norm_rope_store(qkv_b, pos, qw, kw, eps, cs, hq, hkv, hd,
-                                                        kc_h, vc_h, sl), 5)
-        leg["cpu_baseline"] = {"value": round(pbytes / t / 1e9, 4), "unit": "GB/s", "cores": 1,
-                               "kind": "port",
-                               "sample": "the full 4288-token prologue through the numpy oracle "
-                                         "(norms, rotation, store), median of 5 reps on 1 host "
-                                         "thread"}
+        def prologue_cpu():
+            from oracle import torch_cpu as tcpu
+            threads = host_threads(torch)
+            log(f"cpu baseline: prologue on the PyTorch CPU path, {threads} threads")
+            kc_h = torch.zeros(pc.pool_blocks, pc.block_size, hkv, hd, dtype=torch.bfloat16)
+            vc_h = torch.zeros_like(kc_h)
+            cs = pc.cos_sin.reshape(-1, hd)
+            t = cpu_time(lambda: tcpu.qk_norm_rope_store_cpu(
+                pc.positions, pc.qkv, hq, hkv, hd, pc.q_weight, pc.k_weight, eps, cs, kc_h, vc_h,
+                pc.slot_mapping), 10)
+            return {"value": round(pbytes / t / 1e9, 4), "unit": "GB/s", "cores": threads,
+                    "kind": "port",
+                    "sample": "the full 4288-token prologue through the PyTorch CPU path (the "
+                              "reference's RMSNorm and rotary tensor operations, then index_put "
+                              f"into the caches), median of 10 reps on {threads} host threads "
+                              f"(os.cpu_count() = {os.cpu_count()})"}
+        cpu_jobs.append(("prologue", prologue_cpu))
     del copies, fused, unfused
     return leg
 
@@ -480,6 +641,19 @@ def sampler_leg(torch, dev, args):
     return out
 
 
+def copy_ceiling(torch, dev, nbytes, args):
+    """GB/s of torch's device-to-device copy of nbytes (read nbytes + write
+    nbytes) under the same >= 1 GiB rotation as the legs: the read + write rate
+    this box reaches for a transfer of that size."""
+    n = rotation(2 * nbytes)
+    src = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(n)]
+    dst = [torch.empty_like(x) for x in src]
+    fns = [(lambda a=a, b=b: b.copy_(a)) for a, b in zip(src, dst)]
+    _, ev = time_graph(torch, fns, 20, 3, args.eager)
+    del src, dst, fns
+    return round(2 * nbytes / ev / 1e9, 1)
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -487,8 +661,10 @@ def main():
         print("bench.py measures one GPU: the KV-cache path runs on a single MI355X "
               "(no sharding is built); run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.collect_traffic:
+        collect_traffic(*args.collect_traffic)
+        return
 
-    import numpy as np
     import torch
 
     if args.copy_calibration:
@@ -510,8 +686,13 @@ def main():
     legs = set(args.legs.split(","))
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
     result = {}
+    # CPU baselines: (result key, fn -> cpu_baseline dict), run after every GPU leg
+    cpu_jobs = []
+
+    def cpu_sample(n_reps, what, threads):
+        return (f"{what}, median of {n_reps} reps on {threads} host threads "
+                f"(os.cpu_count() = {os.cpu_count()})")
 
     # ------------------------------------------------------------------ decode
     log("building decode workload (B=64, ctx U{100..2048}, 1024-page pool)")
@@ -525,24 +706,22 @@ def main():
         for c, o in zip(pools, outs)]
     log("timing decode")
     wall, ev = time_graph(torch, dec_fns, args.steps, args.warmup, args.eager)
-    dec_gbs = dec_bytes / wall / 1e9
-    dec_ach = dec_bytes / ev / 1e9
-    result["decode"] = dict(ms_per_step=wall * 1e3, gbs=dec_gbs, event_gbs=dec_ach,
-                            bytes_per_step=dec_bytes)
-    cpu = None
-    if not args.no_cpu_baseline:
-        threads = host_threads(torch)
-        log(f"cpu baseline: decode on the PyTorch CPU path, {threads} threads")
-        t = cpu_time(lambda: tcpu.paged_attention_cpu(dc.q, dc.k_cache, dc.v_cache, range(65),
-                                                      dc.context_lens, dc.scale,
-                                                      dc.block_tables), 10)
-        cpu = {"value": round(dec_bytes / t / 1e9, 4), "unit": "GB/s", "cores": threads,
-               "kind": "port",
-               "sample": "the full 64-sequence decode batch through the PyTorch CPU path "
-                         "(block-table gather + f32 scaled_dot_product_attention), median of "
-                         f"10 reps on {threads} host threads "
-                         f"(os.cpu_count() = {os.cpu_count()})"}
+    result["decode"] = dict(ms_per_step=wall * 1e3, gbs=dec_bytes / wall / 1e9,
+                            event_gbs=dec_bytes / ev / 1e9, bytes_per_step=dec_bytes)
     del pools, outs, dec_fns
+    if not args.no_cpu_baseline:
+        def decode_cpu():
+            threads = host_threads(torch)
+            log(f"cpu baseline: decode on the PyTorch CPU path, {threads} threads")
+            t = cpu_time(lambda: tcpu.paged_attention_cpu(dc.q, dc.k_cache, dc.v_cache, range(65),
+                                                          dc.context_lens, dc.scale,
+                                                          dc.block_tables), 10)
+            return {"value": round(dec_bytes / t / 1e9, 4), "unit": "GB/s", "cores": threads,
+                    "kind": "port",
+                    "sample": cpu_sample(10, "the full 64-sequence decode batch through the "
+                                             "PyTorch CPU path (block-table gather + f32 "
+                                             "scaled_dot_product_attention)", threads)}
+        cpu_jobs.append(("decode", decode_cpu))
 
     # ------------------------------------------------------------------ store
     if "store" in legs:
@@ -555,28 +734,38 @@ def main():
                   for c in copies]
         log("timing kv-store")
         wall_s, ev_s = time_graph(torch, st_fns, args.steps, args.warmup, args.eager)
-        leg = dict(ms_per_step=wall_s * 1e3, bytes_per_step=st_bytes,
-                   roofline={"bound": "hbm", "achieved": round(st_bytes / ev_s / 1e9, 2),
-                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                             "frac": round(st_bytes / ev_s / 1e9 / HBM_PEAK_GBS, 4),
-                             "traffic": traffic_for("kv_store")})
-        if not args.no_cpu_baseline:
-            threads = host_threads(torch)
-            kc, vc = sc.k_cache.clone(), sc.v_cache.clone()
-            t = cpu_time(lambda: tcpu.store_kvcache_cpu(sc.key, sc.value, kc, vc,
-                                                        sc.slot_mapping), 50)
-            leg["cpu_baseline"] = {"value": round(st_bytes / t / 1e9, 3), "unit": "GB/s",
-                                   "cores": threads, "kind": "port",
-                                   "sample": "full 4096-token store through the PyTorch CPU "
-                                             "path (index_put on the flat cache views), median "
-                                             f"of 50 reps on {threads} host threads "
-                                             f"(os.cpu_count() = {os.cpu_count()})"}
-        result["kv_store"] = leg
         del copies, st_fns
+        log("timing device copies of the same bytes and of 512 MiB")
+        same = copy_ceiling(torch, dev, st_bytes // 2, args)
+        big = copy_ceiling(torch, dev, 512 << 20, args)
+        ach = st_bytes / ev_s / 1e9
+        result["kv_store"] = dict(
+            ms_per_step=wall_s * 1e3, bytes_per_step=st_bytes,
+            roofline={"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS,
+                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                      "traffic": traffic_for("kv_store")},
+            copy_ceiling={"same_bytes_copy_gbs": same, "copy_512mib_gbs": big,
+                          "frac_of_same_bytes_copy": round(ach / same, 4),
+                          "frac_of_512mib_copy": round(ach / big, 4),
+                          "what": "torch device-to-device copy reading and writing the store's "
+                                  "bytes (and 512 MiB), same rotation, GB/s of read + write"})
+        if not args.no_cpu_baseline:
+            def store_cpu():
+                threads = host_threads(torch)
+                log(f"cpu baseline: kv-store on the PyTorch CPU path, {threads} threads")
+                kc, vc = sc.k_cache.clone(), sc.v_cache.clone()
+                t = cpu_time(lambda: tcpu.store_kvcache_cpu(sc.key, sc.value, kc, vc,
+                                                            sc.slot_mapping), 50)
+                return {"value": round(st_bytes / t / 1e9, 3), "unit": "GB/s", "cores": threads,
+                        "kind": "port",
+                        "sample": cpu_sample(50, "full 4096-token store through the PyTorch CPU "
+                                                 "path (index_put on the flat cache views)",
+                                             threads)}
+            cpu_jobs.append(("kv_store", store_cpu))
 
     # ------------------------------------------------------------------ prologue
     if "prologue" in legs:
-        result["prologue"] = prologue_leg(torch, dev, args, orc, bits)
+        result["prologue"] = prologue_leg(torch, dev, args, orc, cpu_jobs)
 
     # ------------------------------------------------------------------ prefill
     if "prefill" in legs:
@@ -595,27 +784,28 @@ def main():
         log("timing prefill")
         wall_p, ev_p = time_graph(torch, pf_fns, args.steps, args.warmup, args.eager)
         tf = flops / ev_p / 1e12
-        leg = dict(ms_per_step=wall_p * 1e3, flops_per_step=flops,
-                   roofline={"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
-                             "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
-                             "traffic": traffic_for("prefill")})
-        if not args.no_cpu_baseline:
-            threads = host_threads(torch)
-            kc, vc = pc.k_cache.clone(), pc.v_cache.clone()
-            tcpu.store_kvcache_cpu(pc.key, pc.value, kc, vc, pc.slot_mapping)
-            t = cpu_time(lambda: tcpu.paged_attention_cpu(pc.q, kc, vc, pc.cu_seqlens_q,
-                                                          pc.lens_k, pc.scale,
-                                                          pc.block_tables), 5)
-            leg["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
-                                   "cores": threads, "kind": "port",
-                                   "sample": "the full 32-sequence prefill through the PyTorch "
-                                             "CPU path (block-table gather + f32 "
-                                             "scaled_dot_product_attention with the "
-                                             "bottom-right causal mask), median of 5 reps on "
-                                             f"{threads} host threads "
-                                             f"(os.cpu_count() = {os.cpu_count()})"}
-        result["prefill"] = leg
+        result["prefill"] = dict(
+            ms_per_step=wall_p * 1e3, flops_per_step=flops,
+            roofline={"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
+                      "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                      "traffic": traffic_for("prefill")})
         del copies, outs, pf_fns
+        if not args.no_cpu_baseline:
+            def prefill_cpu():
+                threads = host_threads(torch)
+                log(f"cpu baseline: prefill on the PyTorch CPU path, {threads} threads")
+                kc, vc = pc.k_cache.clone(), pc.v_cache.clone()
+                tcpu.store_kvcache_cpu(pc.key, pc.value, kc, vc, pc.slot_mapping)
+                t = cpu_time(lambda: tcpu.paged_attention_cpu(pc.q, kc, vc, pc.cu_seqlens_q,
+                                                              pc.lens_k, pc.scale,
+                                                              pc.block_tables), 5)
+                return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
+                        "cores": threads, "kind": "port",
+                        "sample": cpu_sample(5, "the full 32-sequence prefill through the "
+                                                "PyTorch CPU path (block-table gather + f32 "
+                                                "scaled_dot_product_attention with the "
+                                                "bottom-right causal mask)", threads)}
+            cpu_jobs.append(("prefill", prefill_cpu))
 
     # ------------------------------------------------------------------ spec verify
     if "spec" in legs:
@@ -642,6 +832,22 @@ def main():
                       "frac": round(sv_bytes / ev_v / 1e9 / HBM_PEAK_GBS, 4),
                       "traffic": traffic_for("spec_verify")})
         del copies, outs, sv_fns
+        if not args.no_cpu_baseline:
+            def spec_cpu():
+                threads = host_threads(torch)
+                log(f"cpu baseline: spec verify on the PyTorch CPU path, {threads} threads")
+                kc, vc = vc_.k_cache.clone(), vc_.v_cache.clone()
+                tcpu.store_kvcache_cpu(vc_.key, vc_.value, kc, vc, vc_.slot_mapping)
+                t = cpu_time(lambda: tcpu.paged_attention_cpu(vc_.q, kc, vc, vc_.cu_seqlens_q,
+                                                              vc_.lens_k, vc_.scale,
+                                                              vc_.block_tables), 5)
+                return {"value": round(sv_bytes / t / 1e9, 4), "unit": "GB/s", "cores": threads,
+                        "kind": "port",
+                        "sample": cpu_sample(5, "the full 32 x 6-query verification through "
+                                                "the PyTorch CPU path (block-table gather + f32 "
+                                                "scaled_dot_product_attention with the "
+                                                "bottom-right causal mask)", threads)}
+            cpu_jobs.append(("spec_verify", spec_cpu))
 
     # ------------------------------------------------------------------ decode graphs
     if "graph" in legs:
@@ -657,7 +863,17 @@ def main():
 
     # ------------------------------------------------------------------ mixed step
     if "mixed" in legs:
-        result["mixed_step"] = mixed_leg(torch, dev, args, orc)
+        result["mixed_step"] = mixed_leg(torch, dev, args, orc, cpu_jobs)
+
+    # ------------------------------------------------------------------ CPU baselines
+    torch.cuda.synchronize()
+    cpu = None
+    for key, fn in cpu_jobs:
+        base = fn()
+        if key == "decode":
+            cpu = base
+        else:
+            result[key]["cpu_baseline"] = base
 
     d = result["decode"]
     line = {

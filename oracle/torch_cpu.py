@@ -14,10 +14,16 @@ torch is given), never part of the product.
                         scaled_dot_product_attention in float32 with GQA and the
                         bottom-right aligned causal mask (key j visible to query
                         row i iff j <= i + Lk - Lq); rows that see no key are 0.
+  qk_norm_rope_store_cpu  the attention prologue of Qwen3Attention.forward,
+                        nanovllm/models/qwen3.py:79-86 (split, RMSNorm.rms_forward
+                        layernorm.py:16-26, apply_rotary_emb rotary_embedding.py:6-14
+                        as eager tensor operations) and the store of
+                        attention.py:62-63 (store_kvcache_cpu).
 
 Pinned by tests/test_oracle_torch_cpu.py against oracle/kv_oracle.py (store
-bit for bit, attention to float32 rounding), which the golden vectors and
-closed forms pin in turn.
+bit for bit, attention to float32 rounding, the prologue to the rounding of
+the norm's sum of squares), which the golden vectors and closed forms pin in
+turn.
 """
 from __future__ import annotations
 
@@ -71,3 +77,35 @@ def paged_attention_cpu(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
             o = torch.where(seen[:, None, None], o, torch.zeros((), dtype=o.dtype))
         out[q0:q1] = o
     return out
+
+
+def qk_norm_rope_store_cpu(positions: torch.Tensor, qkv: torch.Tensor, num_q_heads: int,
+                           num_kv_heads: int, head_dim: int, q_weight: torch.Tensor,
+                           k_weight: torch.Tensor, eps: float, cos_sin: torch.Tensor,
+                           k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           slot_mapping: torch.Tensor):
+    """qkv [T, (Hq + 2 Hkv) D] bf16, positions int64 [T], cos_sin float32
+    [max_position, D] (cos | sin halves).  Returns (q, k, v) [T, H, D] bf16
+    and stores k, v at slot_mapping (-1 skipped)."""
+    t = qkv.shape[0]
+    qs, ks = num_q_heads * head_dim, num_kv_heads * head_dim
+    q, k, v = qkv.split([qs, ks, ks], dim=-1)
+    q, k, v = (q.reshape(t, num_q_heads, head_dim), k.reshape(t, num_kv_heads, head_dim),
+               v.reshape(t, num_kv_heads, head_dim))
+
+    def rms(x, w):                                   # layernorm.py:16-26
+        dt = x.dtype
+        x = x.float()
+        var = x.pow(2).mean(dim=-1, keepdim=True)
+        x.mul_(torch.rsqrt(var + eps))
+        return x.to(dt).mul_(w)
+
+    def rope(x, cos, sin):                           # rotary_embedding.py:6-14
+        x1, x2 = torch.chunk(x.float(), 2, dim=-1)
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+    q, k = rms(q, q_weight), rms(k, k_weight)
+    cos, sin = cos_sin[positions].unsqueeze(1).chunk(2, dim=-1)
+    q, k = rope(q, cos, sin), rope(k, cos, sin)
+    store_kvcache_cpu(k, v, k_cache, v_cache, slot_mapping)
+    return q, k, v

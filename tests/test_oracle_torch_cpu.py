@@ -3,7 +3,9 @@ baseline) against oracle/kv_oracle.py, which tests/test_oracle.py pins against
 golden vectors and closed forms: the store bit for bit, attention to float32
 rounding, on the cases the reference's shapes produce (prefix + new tokens
 with bottom-right causal alignment, decode, rows and sequences without keys,
-GQA group sizes 1-8, several page sizes)."""
+GQA group sizes 1-8, several page sizes), and the q/k norm + rotary + store
+prologue (v rows bit for bit; q and k bit for bit but where the sum of
+squares rounds differently, within 2 bf16 ulps)."""
 import numpy as np
 import pytest
 import torch
@@ -84,3 +86,31 @@ def test_bottom_right_alignment_is_what_is_timed():
     top_left = torch.nn.functional.scaled_dot_product_attention(
         q.float().transpose(0, 1), k, v, is_causal=True, scale=scale, enable_gqa=True)
     assert not np.allclose(top_left.transpose(0, 1).numpy(), ref, atol=2e-2, rtol=1e-2)
+
+
+def test_prologue_matches_numpy_oracle():
+    from nanovllm_amd.layers.prologue import rope_cos_sin_cache
+    g = torch.Generator().manual_seed(11)
+    t, hq, hkv, nb, bs = 300, 16, 8, 4, 256
+    qkv = (torch.randn(t, (hq + 2 * hkv) * HD, generator=g) * 2).to(torch.bfloat16)
+    pos = torch.randint(0, 4000, (t,), generator=g)
+    qw = (1 + 0.2 * torch.randn(HD, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.2 * torch.randn(HD, generator=g)).to(torch.bfloat16)
+    cs = rope_cos_sin_cache(HD, 4096, 1e6).reshape(4096, HD)
+    slots = torch.randperm(nb * bs, generator=g)[:t].to(torch.int32)
+    slots[:7] = -1
+    kc = torch.zeros(nb, bs, hkv, HD, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    kc_ref, vc_ref = _bits(kc).copy(), _bits(vc).copy()
+    q, k, v = torch_cpu.qk_norm_rope_store_cpu(pos, qkv, hq, hkv, HD, qw, kw, 1e-6, cs, kc, vc,
+                                               slots)
+    q_ref, k_ref, _ = orc.qk_norm_rope_store(_bits(qkv), pos.numpy(), _bits(qw), _bits(kw), 1e-6,
+                                             cs.numpy(), hq, hkv, HD, kc_ref, vc_ref,
+                                             slots.numpy())
+    assert np.array_equal(_bits(vc), vc_ref)                 # v rows are a bit copy
+    for got, ref in ((q, q_ref), (k, k_ref), (kc, kc_ref)):
+        gb, rb = _bits(got), np.asarray(ref)
+        same = gb == rb
+        assert same.mean() > 0.999                           # sum-of-squares rounding only
+        diff = np.abs(orc.bf16_to_f32(gb) - orc.bf16_to_f32(rb))
+        assert float(diff.max()) <= 2 ** -5 * max(1.0, float(np.abs(orc.bf16_to_f32(rb)).max()))
