@@ -302,6 +302,7 @@ def mixed_leg(torch, dev, args, orc, cpu_jobs, layers=28):
     the GPU) and the same block tables / slots; a layer = KV-store of every new
     token, the prefill chunks, the decodes."""
     from nanovllm_amd import paged_decode, store_kvcache, varlen_prefill
+    from nanovllm_amd.flash_api import prefill_tile_order
     from nanovllm_amd.workloads import mixed_step_metadata
 
     log(f"building mixed step ({layers} layers, ~3.5 GB of KV pool per layer)")
@@ -325,11 +326,15 @@ def mixed_leg(torch, dev, args, orc, cpu_jobs, layers=28):
     scale = 128 ** -0.5
 
     def step():
+        # the layers share the step's metadata: the prefill tiles are ranked once
+        order = prefill_tile_order(t["cu_seqlens_q"], t["cu_seqlens_k"], meta["max_seqlen_q"],
+                                   pools[0][0], block_table=t["prefill_block_tables"],
+                                   max_seqlen_k=meta["max_seqlen_k"])
         for kc, vc in pools:
             store_kvcache(key, value, kc, vc, t["slot_mapping"])
             varlen_prefill(q_pf, kc, vc, t["cu_seqlens_q"], t["cu_seqlens_k"],
                            meta["max_seqlen_q"], scale, block_table=t["prefill_block_tables"],
-                           out=o_pf, max_seqlen_k=meta["max_seqlen_k"])
+                           out=o_pf, max_seqlen_k=meta["max_seqlen_k"], order=order)
             paged_decode(q_dec, kc, vc, t["context_lens"], t["decode_block_tables"], scale,
                          out=o_dec)
 
@@ -347,7 +352,7 @@ def mixed_leg(torch, dev, args, orc, cpu_jobs, layers=28):
     return dict(ms_per_step=wall * 1e3, layers=layers, steps=steps,
                 workload="28 layers x (KV-store 4288 tokens + 8 prefill chunks of 512 after "
                          "U{0..1536} cached + 192 decodes over U{256..4096}), 3300-page pool "
-                         "per layer",
+                         "per layer; prefill tiles ranked once per step",
                 per_layer={"decode_bytes": dec_bytes, "prefill_flops": pf_flops,
                            "store_bytes": st_bytes},
                 roofline={"bound": "mixed", "t_roof_ms": round(t_roof * 1e3, 4),

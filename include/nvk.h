@@ -33,8 +33,10 @@
  *   - Return value: 0 = enqueued; a negative NVK_E* code = the arguments were
  *     rejected before anything was launched; a positive value = the hipError_t
  *     reported by the launch.
- *   - The library keeps no pointer after it returns and has no global state,
- *     so calls from several host threads on distinct streams are independent.
+ *   - The library keeps no pointer after it returns and has no global state
+ *     but the static scratch of nvk_paged_decode_noalloc (one per GPU), so
+ *     calls from several host threads on distinct streams, each with its own
+ *     workspace, are independent.
  *   - KV-cache layout (nanovllm/engine/model_runner.py:115-121): per layer
  *     k_cache / v_cache are contiguous [num_blocks][block_size][num_kv_heads][head_dim];
  *     the flat token slot s = page * block_size + offset addresses row s of a
@@ -234,6 +236,49 @@ size_t nvk_varlen_prefill_workspace_size(int32_t batch, int32_t max_seqlen_q,
                                          int32_t num_kv_heads, int32_t head_dim);
 
 /*
+ * The longest-first order of a prefill's query tiles, ranked once for every
+ * layer of a step.  Every decoder layer of a model step calls the prefill
+ * with the same cu_seqlens (nanovllm/layers/attention.py:67-70, once per
+ * layer of nanovllm/models/qwen3.py:180-181); nvk_varlen_prefill ranks them
+ * in each call, these rank them once.
+ *
+ * nvk_prefill_tile_order_size: bytes of the order a prefill of these sizes
+ *   uses, 0 when it runs its query tiles in grid order (few tiles, short
+ *   query ranges split across workgroups or taken by the short-query
+ *   kernels).  max_keys: the per-sequence key bound the prefill call will
+ *   use (min(max_seqlen_k, max_blocks*block_size) paged, min(max_seqlen_k,
+ *   total_k) dense); block_size: the page size, 0 for dense keys.
+ * nvk_prefill_tile_order: writes that order (one kernel; nothing when the
+ *   size is 0).  order: device int32, 16-byte aligned, order_bytes >= size.
+ * nvk_varlen_prefill_ordered: nvk_varlen_prefill with the order given; it
+ *   launches no ranking kernel.  The order must come from
+ *   nvk_prefill_tile_order with the same cu_seqlens_q / cu_seqlens_k, batch,
+ *   max_seqlen_q, key bound and head counts (else the output is
+ *   unspecified; no access goes out of bounds).  NULL = nvk_varlen_prefill.
+ *   Outputs are bit-identical to nvk_varlen_prefill's.
+ */
+size_t nvk_prefill_tile_order_size(int32_t batch, int32_t max_seqlen_q, int32_t max_keys,
+                                   int32_t num_q_heads, int32_t num_kv_heads, int32_t block_size);
+int nvk_prefill_tile_order(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                           int32_t batch, int32_t max_seqlen_q, int32_t max_keys,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t block_size,
+                           int32_t* order, size_t order_bytes, void* stream);
+int nvk_varlen_prefill_ordered(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                               int64_t total_q,
+                               const void* k, const void* v,
+                               int64_t k_stride_tok, int64_t v_stride_tok,
+                               int64_t kv_stride_head, int64_t total_k,
+                               const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                               int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                               const int32_t* block_tables, int64_t bt_stride,
+                               int32_t max_blocks, int32_t block_size, int32_t num_blocks,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               float scale,
+                               void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                               void* workspace, size_t workspace_bytes, const int32_t* order,
+                               int32_t dtype, void* stream);
+
+/*
  * Fused attention prologue: q/k RMSNorm + rotary embedding + KV-store.
  * Replaces, per decoder layer, the steps between the qkv projection and the
  * attention kernels: nanovllm/models/qwen3.py:79-86 (split, q_norm, k_norm,
@@ -342,6 +387,17 @@ int nvk_decode_metadata(const int32_t* seq_lens, const int32_t* bt_offsets,
                         int32_t block_size, int32_t table_width, int64_t table_row_stride,
                         int32_t* context_lens, int64_t* positions, int32_t* slot_mapping,
                         int32_t* block_tables, void* stream);
+
+/*
+ * cu_seqlens of a query block of seqlen_q tokens at the end of every
+ * sequence's seqlens_k[b] keys (speculative-decode verification through
+ * flash_attn_with_kvcache with seqlen_q > 1, whose cache_seqlens
+ * nanovllm/layers/attention.py:72-74 passes): cu_seqlens_q[b] = b*seqlen_q,
+ * cu_seqlens_k = exclusive prefix of seqlens_k ([batch+1] int32 each).  One
+ * kernel; batch <= 8192.
+ */
+int nvk_uniform_cu_seqlens(const int32_t* seqlens_k, int32_t batch, int32_t seqlen_q,
+                           int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, void* stream);
 
 /*
  * LM-head last-token gather (nanovllm/layers/embed_head.py:56-60): in a

@@ -151,6 +151,22 @@ __global__ __launch_bounds__(kThreads) void decode_metadata_kernel(DecodeMetaArg
   write_tables(a.bt_off, a.bt_ids, a.batch, a.width, a.table_stride, a.tables);
 }
 
+// cu_seqlens of a uniform query block per sequence over its cache lengths
+// (seqlen_q queries at the end of each sequence's seqlens_k keys): one
+// workgroup, cu_q[b] = b * seqlen_q, cu_k = exclusive prefix of seqlens_k.
+__global__ __launch_bounds__(kThreads) void uniform_cu_seqlens_kernel(const int32_t* seqlens_k,
+                                                                     int B, int seqlen_q,
+                                                                     int32_t* cu_q,
+                                                                     int32_t* cu_k) {
+  __shared__ int s_cu[kMaxBatch + 1];
+  __shared__ int s_wsum[kThreads / 64];
+  block_prefix([&](int b) { return seqlens_k[b]; }, B, s_cu, s_wsum);
+  for (int b = threadIdx.x; b <= B; b += kThreads) {
+    cu_q[b] = b * seqlen_q;
+    cu_k[b] = s_cu[b];
+  }
+}
+
 }  // namespace
 
 extern "C" int nvk_prefill_metadata(const int32_t* num_cached, const int32_t* num_new,
@@ -219,5 +235,17 @@ extern "C" int nvk_decode_metadata(const int32_t* seq_lens, const int32_t* bt_of
   grid = grid < 1 ? 1 : (grid > kMaxGrid ? kMaxGrid : grid);
   hipLaunchKernelGGL(decode_metadata_kernel, dim3((unsigned)grid), dim3(kThreads), 0,
                      reinterpret_cast<hipStream_t>(stream), a);
+  return nvk_launch_status();
+}
+
+extern "C" int nvk_uniform_cu_seqlens(const int32_t* seqlens_k, int32_t batch, int32_t seqlen_q,
+                                      int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
+                                      void* stream) {
+  if (batch < 0 || seqlen_q < 0 || batch > kMaxBatch) return NVK_EINVAL;
+  if ((int64_t)batch * seqlen_q > INT32_MAX) return NVK_EINVAL;
+  if (!cu_seqlens_q || !cu_seqlens_k || (batch > 0 && !seqlens_k)) return NVK_EINVAL;
+  hipLaunchKernelGGL(uniform_cu_seqlens_kernel, dim3(1), dim3(kThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), seqlens_k, batch, seqlen_q,
+                     cu_seqlens_q, cu_seqlens_k);
   return nvk_launch_status();
 }

@@ -879,18 +879,34 @@ extern "C" size_t nvk_varlen_prefill_workspace_size(int32_t batch, int32_t max_s
   return ord > need ? ord : need;
 }
 
-extern "C" int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
-                                  int64_t total_q, const void* k, const void* v,
-                                  int64_t k_stride_tok, int64_t v_stride_tok,
-                                  int64_t kv_stride_head, int64_t total_k,
-                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                                  int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k,
-                                  const int32_t* block_tables, int64_t bt_stride,
-                                  int32_t max_blocks, int32_t block_size, int32_t num_blocks,
-                                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                                  float scale, void* out, int64_t out_stride_tok,
-                                  int64_t out_stride_head, void* workspace,
-                                  size_t workspace_bytes, int32_t dtype, void* stream) {
+namespace {
+
+// Bytes of the longest-first order a launch of these sizes uses (0: it runs
+// its query tiles in grid order).  The same decision varlen_prefill_impl takes.
+size_t order_bytes_for(int32_t batch, int32_t max_seqlen_q, int64_t max_keys, int32_t num_q_heads,
+                       int32_t num_kv_heads, bool paged, int32_t block_size) {
+  if (batch <= 0 || max_seqlen_q <= 0 || max_keys <= 0 || num_q_heads <= 0 ||
+      num_kv_heads <= 0 || num_q_heads % num_kv_heads)
+    return 0;
+  if (paged && short_query_applies(true, block_size, max_seqlen_q, num_q_heads, num_kv_heads, HD,
+                                   batch))
+    return 0;  // the short-query kernels take these
+  const SplitPlan sp = plan_splits(batch, max_seqlen_q, max_keys, num_q_heads, num_kv_heads);
+  const int64_t pairs = (int64_t)batch * sp.n_qtiles;
+  if (sp.n_splits != 1 || !use_order(batch, pairs, num_kv_heads)) return 0;
+  return order_bytes(pairs);
+}
+
+int varlen_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                        int64_t total_q, const void* k, const void* v, int64_t k_stride_tok,
+                        int64_t v_stride_tok, int64_t kv_stride_head, int64_t total_k,
+                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t batch,
+                        int32_t max_seqlen_q, int32_t max_seqlen_k, const int32_t* block_tables,
+                        int64_t bt_stride, int32_t max_blocks, int32_t block_size,
+                        int32_t num_blocks, int32_t num_q_heads, int32_t num_kv_heads,
+                        int32_t head_dim, float scale, void* out, int64_t out_stride_tok,
+                        int64_t out_stride_head, void* workspace, size_t workspace_bytes,
+                        int32_t dtype, void* stream, const int32_t* given_order) {
   if (batch < 0 || max_seqlen_q < 0 || max_seqlen_k < 0 || num_q_heads <= 0 ||
       num_kv_heads <= 0 || total_q < 0 || total_k < 0)
     return NVK_EINVAL;
@@ -997,14 +1013,17 @@ extern "C" int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q
   // sequence: the grid order (last query tile first) already is.
   a.order = nullptr;
   const int64_t pairs = (int64_t)batch * sp.n_qtiles;
-  if (sp.n_splits == 1 && use_order(batch, pairs, num_kv_heads) && workspace &&
-      workspace_bytes >= order_bytes(pairs)) {
-    int32_t* order = static_cast<int32_t*>(workspace);
-    hipLaunchKernelGGL(prefill_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, s,
-                       cu_seqlens_q, cu_seqlens_k, batch, sp.n_qtiles, kRows / G, order);
-    const int st = nvk_launch_status();
-    if (st != NVK_OK) return st;
-    a.order = order;
+  if (sp.n_splits == 1 && use_order(batch, pairs, num_kv_heads)) {
+    if (given_order) {
+      a.order = given_order;  // ranked once for every layer of the step
+    } else if (workspace && workspace_bytes >= order_bytes(pairs)) {
+      int32_t* order = static_cast<int32_t*>(workspace);
+      hipLaunchKernelGGL(prefill_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, s,
+                         cu_seqlens_q, cu_seqlens_k, batch, sp.n_qtiles, kRows / G, order);
+      const int st = nvk_launch_status();
+      if (st != NVK_OK) return st;
+      a.order = order;
+    }
   }
   switch (G) {
     case 1: return launch_prefill<1>(a, s);
@@ -1012,4 +1031,69 @@ extern "C" int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q
     case 4: return launch_prefill<4>(a, s);
     default: return launch_prefill<8>(a, s);
   }
+}
+
+}  // namespace
+
+extern "C" int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                  int64_t total_q, const void* k, const void* v,
+                                  int64_t k_stride_tok, int64_t v_stride_tok,
+                                  int64_t kv_stride_head, int64_t total_k,
+                                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int32_t batch, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                                  const int32_t* block_tables, int64_t bt_stride,
+                                  int32_t max_blocks, int32_t block_size, int32_t num_blocks,
+                                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  float scale, void* out, int64_t out_stride_tok,
+                                  int64_t out_stride_head, void* workspace,
+                                  size_t workspace_bytes, int32_t dtype, void* stream) {
+  return varlen_prefill_impl(q, q_stride_tok, q_stride_head, total_q, k, v, k_stride_tok,
+                             v_stride_tok, kv_stride_head, total_k, cu_seqlens_q, cu_seqlens_k,
+                             batch, max_seqlen_q, max_seqlen_k, block_tables, bt_stride,
+                             max_blocks, block_size, num_blocks, num_q_heads, num_kv_heads,
+                             head_dim, scale, out, out_stride_tok, out_stride_head, workspace,
+                             workspace_bytes, dtype, stream, nullptr);
+}
+
+extern "C" int nvk_varlen_prefill_ordered(
+    const void* q, int64_t q_stride_tok, int64_t q_stride_head, int64_t total_q, const void* k,
+    const void* v, int64_t k_stride_tok, int64_t v_stride_tok, int64_t kv_stride_head,
+    int64_t total_k, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t batch,
+    int32_t max_seqlen_q, int32_t max_seqlen_k, const int32_t* block_tables, int64_t bt_stride,
+    int32_t max_blocks, int32_t block_size, int32_t num_blocks, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, float scale, void* out, int64_t out_stride_tok,
+    int64_t out_stride_head, void* workspace, size_t workspace_bytes, const int32_t* order,
+    int32_t dtype, void* stream) {
+  return varlen_prefill_impl(q, q_stride_tok, q_stride_head, total_q, k, v, k_stride_tok,
+                             v_stride_tok, kv_stride_head, total_k, cu_seqlens_q, cu_seqlens_k,
+                             batch, max_seqlen_q, max_seqlen_k, block_tables, bt_stride,
+                             max_blocks, block_size, num_blocks, num_q_heads, num_kv_heads,
+                             head_dim, scale, out, out_stride_tok, out_stride_head, workspace,
+                             workspace_bytes, dtype, stream, order);
+}
+
+extern "C" size_t nvk_prefill_tile_order_size(int32_t batch, int32_t max_seqlen_q,
+                                              int32_t max_keys, int32_t num_q_heads,
+                                              int32_t num_kv_heads, int32_t block_size) {
+  return order_bytes_for(batch, max_seqlen_q, max_keys, num_q_heads, num_kv_heads,
+                         block_size > 0, block_size);
+}
+
+extern "C" int nvk_prefill_tile_order(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                      int32_t batch, int32_t max_seqlen_q, int32_t max_keys,
+                                      int32_t num_q_heads, int32_t num_kv_heads,
+                                      int32_t block_size, int32_t* order, size_t order_bytes_,
+                                      void* stream) {
+  const size_t need = order_bytes_for(batch, max_seqlen_q, max_keys, num_q_heads, num_kv_heads,
+                                      block_size > 0, block_size);
+  if (need == 0) return NVK_OK;  // nothing to rank: the prefill runs in grid order
+  if (!cu_seqlens_q || !cu_seqlens_k || !order) return NVK_EINVAL;
+  if (order_bytes_ < need) return NVK_EWORKSPACE;
+  const int G = num_q_heads / num_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return NVK_EUNSUPPORTED;
+  const SplitPlan sp = plan_splits(batch, max_seqlen_q, max_keys, num_q_heads, num_kv_heads);
+  hipLaunchKernelGGL(prefill_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), cu_seqlens_q, cu_seqlens_k, batch,
+                     sp.n_qtiles, kRows / G, order);
+  return nvk_launch_status();
 }

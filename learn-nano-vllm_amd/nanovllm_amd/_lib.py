@@ -49,6 +49,16 @@ SIGNATURES = {
                                           _c_ptr, ctypes.c_size_t, _c_i32, _c_ptr]),
     "nvk_varlen_prefill_workspace_size": (ctypes.c_size_t,
                                           [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "nvk_prefill_tile_order_size": (ctypes.c_size_t, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                                      _c_i32]),
+    "nvk_prefill_tile_order": (ctypes.c_int, [_c_ptr, _c_ptr, _c_i32, _c_i32, _c_i32, _c_i32,
+                                              _c_i32, _c_i32, _c_ptr, ctypes.c_size_t, _c_ptr]),
+    "nvk_varlen_prefill_ordered": (ctypes.c_int, [_c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr,
+                                                  _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr,
+                                                  _c_i32, _c_i32, _c_i32, _c_ptr, _c_i64, _c_i32,
+                                                  _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                                  ctypes.c_float, _c_ptr, _c_i64, _c_i64, _c_ptr,
+                                                  ctypes.c_size_t, _c_ptr, _c_i32, _c_ptr]),
     "nvk_qk_norm_rope_store": (ctypes.c_int, [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr,
                                               ctypes.c_float, _c_ptr, _c_i64, _c_i64, _c_i32,
                                               _c_i32, _c_i32, _c_ptr, _c_i64, _c_i64, _c_ptr,
@@ -65,6 +75,7 @@ SIGNATURES = {
                                             _c_ptr]),
     "nvk_decode_metadata": (ctypes.c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i32, _c_i32, _c_i32, _c_i32,
                                            _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr]),
+    "nvk_uniform_cu_seqlens": (ctypes.c_int, [_c_ptr, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr]),
     "nvk_sample_workspace_size": (ctypes.c_size_t, [_c_i32, _c_i32]),
     "nvk_sample": (ctypes.c_int, [_c_ptr, _c_i64, _c_i32, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_i64,
                                   ctypes.c_uint64, ctypes.c_uint64, _c_ptr, _c_ptr, ctypes.c_size_t,
@@ -135,3 +146,27 @@ def stream_ptr(device: torch.device) -> int:
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+# Workspaces of the attention wrappers, one per (device, stream), grown on
+# demand: calls on one stream run one after the other, so they can share it
+# (every kernel writes what it reads in the same call).  Buffers a larger one
+# replaces stay referenced, so a graph captured with them keeps valid memory.
+_workspaces: dict = {}
+_retired: list = []
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """A uint8 device buffer of at least nbytes for the current stream of
+    `device` (None for 0 bytes); torch's allocator hands out 512-byte aligned
+    blocks, and under graph capture the buffer comes from the graph's pool."""
+    if nbytes <= 0:
+        return None
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            _retired.append(buf)
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    return buf

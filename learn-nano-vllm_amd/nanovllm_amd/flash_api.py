@@ -33,15 +33,48 @@ def _int32(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
+def _key_bound(k, block_table, max_seqlen_k):
+    """The per-sequence key bound the library plans a prefill with."""
+    bound = (block_table.shape[1] * k.shape[1]) if block_table is not None else k.shape[0]
+    return min(int(max_seqlen_k), bound) if max_seqlen_k else bound
+
+
+def prefill_tile_order(cu_seqlens_q, cu_seqlens_k, max_seqlen_q, k, block_table=None,
+                       max_seqlen_k=None, num_q_heads=16):
+    """The longest-first order of a prefill's query tiles, for every layer of a
+    step (they share cu_seqlens): pass it as ``order`` to varlen_prefill to
+    skip the per-call ranking kernel.  k: the layer's keys or cache (only its
+    shape is read).  Returns an int32 device tensor, or None when the prefill
+    runs in grid order anyway."""
+    dev = _lib.require_gpu(cu_seqlens_q, cu_seqlens_k)
+    cu_q, cu_k = _int32(cu_seqlens_q), _int32(cu_seqlens_k)
+    batch = cu_q.numel() - 1
+    hkv = k.shape[2] if block_table is not None else k.shape[1]
+    bs = k.shape[1] if block_table is not None else 0
+    mk = _key_bound(k, block_table, max_seqlen_k)
+    lib = _lib.load()
+    nbytes = lib.nvk_prefill_tile_order_size(batch, int(max_seqlen_q), mk, num_q_heads, hkv, bs)
+    if nbytes == 0:
+        return None
+    order = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        code = lib.nvk_prefill_tile_order(cu_q.data_ptr(), cu_k.data_ptr(), batch,
+                                          int(max_seqlen_q), mk, num_q_heads, hkv, bs,
+                                          order.data_ptr(), nbytes, _lib.stream_ptr(dev))
+    _lib.check(code)
+    return order
+
+
 def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_scale,
-                   block_table=None, out=None, max_seqlen_k=None):
+                   block_table=None, out=None, max_seqlen_k=None, order=None):
     """Causal varlen attention (bottom-right aligned), dense or paged keys.
 
     q: [Tq, Hq, D]; dense k/v: [Tk, Hkv, D]; paged k/v: [NB, bs, Hkv, D] caches
     with ``block_table`` [B, W] int32.  Returns [Tq, Hq, D] (or fills ``out``).
     ``max_seqlen_k`` (host int, optional) bounds the keys of a sequence; the
     library uses it to decide whether to split long key ranges across
-    workgroups (the workspace for that is allocated here, with torch).
+    workgroups (its workspace is this stream's cached buffer).  ``order``:
+    from prefill_tile_order with the same metadata (ranked once per step).
     """
     dev = _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, block_table)
     _check_bf16(q, k, v)
@@ -81,16 +114,18 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_sc
     key_bound = max_blocks * block_size if bt is not None else total_k
     msk = min(int(max_seqlen_k), key_bound) if max_seqlen_k else key_bound
     ws_bytes = lib.nvk_varlen_prefill_workspace_size(batch, int(max_seqlen_q), msk, hq, hkv, d)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    ws = _lib.workspace(dev, ws_bytes)
+    if order is not None and (order.dtype != torch.int32 or not order.is_cuda):
+        raise _lib.NvkError("order must be the int32 device tensor prefill_tile_order returns")
     with torch.cuda.device(dev):
-        code = lib.nvk_varlen_prefill(
+        code = lib.nvk_varlen_prefill_ordered(
             q.data_ptr(), q.stride(0), q.stride(1), tq,
             k.data_ptr(), v.data_ptr(), k_st, v_st, kv_sh, total_k,
             cu_q.data_ptr(), cu_k.data_ptr(), batch, int(max_seqlen_q), msk,
             _lib.ptr(bt), bt_stride, max_blocks, block_size, num_blocks,
             hq, hkv, d, scale,
             out.data_ptr(), out.stride(0), out.stride(1),
-            _lib.ptr(ws), ws_bytes,
+            _lib.ptr(ws), ws_bytes, _lib.ptr(order),
             _lib.NVK_DTYPE_BF16, _lib.stream_ptr(dev))
     _lib.check(code)
     return out
@@ -119,8 +154,7 @@ def paged_decode(q, k_cache, v_cache, context_lens, block_table, softmax_scale, 
     lib = _lib.load()
     max_blocks = bt.shape[1]
     ws_bytes = lib.nvk_paged_decode_workspace_size(b, hq, hkv, d, block_size, max_blocks)
-    # torch's caching allocator hands out 512-byte aligned blocks (graph-pool safe)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    ws = _lib.workspace(dev, ws_bytes)
     with torch.cuda.device(dev):
         code = lib.nvk_paged_decode(
             q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
@@ -179,9 +213,12 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, rotary_cos=None
     if not causal:
         raise NotImplementedError("nanovllm_amd: seqlen_q > 1 needs causal=True")
     lens = _int32(cache_seqlens)
-    cu_q = torch.arange(0, (b + 1) * sq, sq, dtype=torch.int32, device=dev)
-    cu_k = torch.zeros(b + 1, dtype=torch.int32, device=dev)
-    torch.cumsum(lens, 0, out=cu_k[1:])
+    cu = torch.empty(2, b + 1, dtype=torch.int32, device=dev)   # cu_seqlens_q, cu_seqlens_k
+    with torch.cuda.device(dev):
+        code = _lib.load().nvk_uniform_cu_seqlens(lens.data_ptr(), b, sq, cu[0].data_ptr(),
+                                                  cu[1].data_ptr(), _lib.stream_ptr(dev))
+    _lib.check(code)
+    cu_q, cu_k = cu[0], cu[1]
     qf = q.reshape(b * sq, hq, d)
     out = varlen_prefill(qf, k_cache, v_cache, cu_q, cu_k, sq, softmax_scale,
                          block_table=block_table)

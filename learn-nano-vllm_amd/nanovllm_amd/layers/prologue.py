@@ -146,7 +146,7 @@ def paged_decode_with_prologue(positions: torch.Tensor, qkv: torch.Tensor, num_h
     max_blocks = bt.shape[1]
     ws_bytes = lib.nvk_paged_decode_workspace_size(B, num_heads, num_kv_heads, head_dim,
                                                    block_size, max_blocks)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    ws = _lib.workspace(dev, ws_bytes)
     with torch.cuda.device(dev):
         code = lib.nvk_paged_decode_prologue(
             qkv.data_ptr(), qkv.stride(0), pos.data_ptr(), qw.data_ptr(), kw.data_ptr(),

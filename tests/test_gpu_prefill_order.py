@@ -73,3 +73,42 @@ def test_ordered_many_short_sequences_with_empty_ones():
     assert torch.equal(ordered, grid)
     ref = oracle_prefill_paged(q, kc, vc, bt, cu_q, cu_k, 256, 128 ** -0.5)
     assert_attn_close(ordered, ref, "ordered prefill, 300 short sequences")
+
+
+def test_order_ranked_once_serves_every_layer():
+    """nvk_prefill_tile_order once, then three layers' prefills (their own
+    caches, the same metadata) through nvk_varlen_prefill_ordered: each equals
+    nvk_varlen_prefill, which ranks the tiles itself, bit for bit; the order
+    is a permutation of the (sequence, query tile) pairs."""
+    from nanovllm_amd import _lib, varlen_prefill
+    from nanovllm_amd.flash_api import prefill_tile_order
+    rng = np.random.default_rng(75)
+    lens_q = [int(x) for x in rng.integers(1, 600, 40)]
+    lens_k = [q + int(c) for q, c in zip(lens_q, rng.integers(0, 900, len(lens_q)))]
+    base = _paged_case(76, lens_q, lens_k)
+    q, kc, vc, bt, cu_q, cu_k = base
+    gen = torch.Generator().manual_seed(77)
+    layers = [base] + [(q, torch.randn(kc.shape, generator=gen).to(torch.bfloat16),
+                        torch.randn(vc.shape, generator=gen).to(torch.bfloat16), bt, cu_q, cu_k)
+                       for _ in range(2)]
+    dcu_q, dcu_k, dbt = cu_q.cuda(), cu_k.cuda(), bt.cuda()
+    say("prefill order once per step: rank")
+    order = prefill_tile_order(dcu_q, dcu_k, max(lens_q), kc.cuda(), block_table=dbt,
+                               max_seqlen_k=max(lens_k))
+    assert order is not None
+    pairs = len(lens_q) * ((max(lens_q) + 63) // 64)
+    assert sorted(order[:pairs].cpu().tolist()) == list(range(pairs))
+    for i, (q, kc, vc, bt_i, _, _) in enumerate(layers):
+        assert torch.equal(bt_i, bt)
+        dq, dkc, dvc = q.cuda(), kc.cuda(), vc.cuda()
+        say(f"prefill order once per step: layer {i}")
+        a = varlen_prefill(dq, dkc, dvc, dcu_q, dcu_k, max(lens_q), 128 ** -0.5, block_table=dbt,
+                           max_seqlen_k=max(lens_k), order=order)
+        b = varlen_prefill(dq, dkc, dvc, dcu_q, dcu_k, max(lens_q), 128 ** -0.5, block_table=dbt,
+                           max_seqlen_k=max(lens_k))
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"layer {i}"
+    ref = oracle_prefill_paged(q, kc, vc, bt, cu_q, cu_k, 256, 128 ** -0.5)
+    assert_attn_close(a, ref, "ordered prefill, last layer")
+    # a launch that runs in grid order needs no order
+    assert _lib.load().nvk_prefill_tile_order_size(3, 100, 1536, 16, 8, 256) == 0
