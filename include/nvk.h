@@ -123,7 +123,8 @@ int nvk_kv_store(const void* key, int64_t key_row_stride,
  *   between waves); it need not be initialised, every call writes what it
  *   reads.  Two calls in flight at once need two workspaces.
  * Two kernels are enqueued: the balanced split-K pass and a combine pass.
- * scale must be > 0.  dtype: NVK_DTYPE_BF16.  head_dim: 128 or 64.
+ * scale must be > 0.  dtype: NVK_DTYPE_BF16 or NVK_DTYPE_F16 (q, caches and
+ * out alike; f32 accumulation either way).  head_dim: 128 or 64.
  * G: 1, 2, 4 or 8.  batch <= 2048.  q, k_cache, v_cache and out 16-byte
  * aligned, token / head strides multiples of 8 elements.
  */
@@ -211,7 +212,8 @@ int nvk_paged_decode_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stri
  *   and the attention kernel runs them longest first; without the workspace
  *   they run in grid order, with the same output bits.  Two calls in flight
  *   at once need two workspaces.
- * scale must be > 0.  dtype: NVK_DTYPE_BF16.  head_dim: 128.  G: 1, 2, 4 or 8.
+ * scale must be > 0.  dtype: NVK_DTYPE_BF16 or NVK_DTYPE_F16 (q, k / v and
+ * out alike; f32 accumulation either way).  head_dim: 128.  G: 1, 2, 4 or 8.
  */
 int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                        int64_t total_q,

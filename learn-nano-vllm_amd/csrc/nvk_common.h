@@ -44,6 +44,52 @@ NVK_DEVICE float nvk_dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(nvk_bf16x2, b), c, false);
 }
 
+// ---- 16-bit element types of q / K / V / outputs: bf16 or f16 --------------
+// The attention kernels are written once over this trait: the packing of f32
+// pairs (round to nearest even), the f32-accumulating pair dot product, the
+// MFMA of the element type and the packed pair (1, 1) used for row sums.
+typedef _Float16 nvk_f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 nvk_f16x2 __attribute__((ext_vector_type(2)));
+
+template <bool F16>
+struct NvkElt;
+
+template <>
+struct NvkElt<false> {  // bf16
+  typedef nvk_bf16x8 vec8;
+  static constexpr uint32_t kOnes = 0x3F803F80u;
+  static NVK_DEVICE uint32_t pack2(float lo, float hi) { return nvk_pack_bf16x2(lo, hi); }
+  static NVK_DEVICE float dot2(uint32_t a, uint32_t b, float c) { return nvk_dot2_bf16(a, b, c); }
+  static NVK_DEVICE uint16_t one(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+  static NVK_DEVICE nvk_f32x16 mfma32x32x16(vec8 a, vec8 b, nvk_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static NVK_DEVICE nvk_f32x4 mfma16x16x32(vec8 a, vec8 b, nvk_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct NvkElt<true> {  // f16
+  typedef nvk_f16x8 vec8;
+  static constexpr uint32_t kOnes = 0x3C003C00u;
+  static NVK_DEVICE uint32_t pack2(float lo, float hi) {
+    nvk_f16x2 p = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, p);
+  }
+  static NVK_DEVICE float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(nvk_f16x2, a),
+                                  __builtin_bit_cast(nvk_f16x2, b), c, false);
+  }
+  static NVK_DEVICE uint16_t one(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+  static NVK_DEVICE nvk_f32x16 mfma32x32x16(vec8 a, vec8 b, nvk_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static NVK_DEVICE nvk_f32x4 mfma16x16x32(vec8 a, vec8 b, nvk_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
 // ---- cross-lane reductions -------------------------------------------------
 // DPP controls (GFX9 encoding): quad_perm xor1 / xor2, row_half_mirror, row_mirror.
 #define NVK_DPP_QP_XOR1 0xB1

@@ -95,6 +95,7 @@ struct DecodeArgs {
   int64_t cache_slots;
   uint16_t* k_store;  // the caches, written at the slots
   uint16_t* v_store;
+  bool f16;           // elements are f16 (else bf16)
 };
 
 // context_lens and block_tables are read-only for the whole launch: read them
@@ -336,21 +337,22 @@ struct SoftmaxState {
   }
 };
 
-template <int HD, int G>
+template <int HD, int G, bool F16>
 __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, const ChunkBuf<HD, G>& buf,
                                               int base, int ctx, int tpi, const LaneRole& r,
                                               SoftmaxState<G>& st) {
   using CB = ChunkBuf<HD, G>;
+  using E = NvkElt<F16>;
   float s[G][kLoads];
 #pragma unroll
   for (int i = 0; i < kLoads; ++i) {
     const bool ok = base + i * tpi + r.tt < ctx;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float acc = nvk_dot2_bf16(buf.q[h][0], buf.k[i].x, 0.f);
-      acc = nvk_dot2_bf16(buf.q[h][1], buf.k[i].y, acc);
-      acc = nvk_dot2_bf16(buf.q[h][2], buf.k[i].z, acc);
-      acc = nvk_dot2_bf16(buf.q[h][3], buf.k[i].w, acc);
+      float acc = E::dot2(buf.q[h][0], buf.k[i].x, 0.f);
+      acc = E::dot2(buf.q[h][1], buf.k[i].y, acc);
+      acc = E::dot2(buf.q[h][2], buf.k[i].z, acc);
+      acc = E::dot2(buf.q[h][3], buf.k[i].w, acc);
       acc = nvk_group_sum<CB::LPR>(acc);
       s[h][i] = ok ? acc * a.scale_log2 : -INFINITY;
     }
@@ -378,7 +380,7 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, const ChunkBu
   for (int i = 0; i < kLoads; i += 2) {
     uint32_t pk[G];
 #pragma unroll
-    for (int h = 0; h < G; ++h) pk[h] = nvk_pack_bf16x2(s[h][i], s[h][i + 1]);
+    for (int h = 0; h < G; ++h) pk[h] = E::pack2(s[h][i], s[h][i + 1]);
     const uint32_t va[4] = {buf.v[i].x, buf.v[i].y, buf.v[i].z, buf.v[i].w};
     const uint32_t vb[4] = {buf.v[i + 1].x, buf.v[i + 1].y, buf.v[i + 1].z, buf.v[i + 1].w};
 #pragma unroll
@@ -387,8 +389,8 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, const ChunkBu
       const uint32_t odd = __builtin_amdgcn_perm(vb[w], va[w], 0x07060302u);   // (va.hi, vb.hi)
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        st.o[h][2 * w] = nvk_dot2_bf16(pk[h], even, st.o[h][2 * w]);
-        st.o[h][2 * w + 1] = nvk_dot2_bf16(pk[h], odd, st.o[h][2 * w + 1]);
+        st.o[h][2 * w] = E::dot2(pk[h], even, st.o[h][2 * w]);
+        st.o[h][2 * w + 1] = E::dot2(pk[h], odd, st.o[h][2 * w + 1]);
       }
     }
   }
@@ -417,17 +419,20 @@ __device__ __forceinline__ void merge_same_head(SoftmaxState<G>& st, int tpi, in
   }
 }
 
-__device__ __forceinline__ void store_bf16x8(uint16_t* p, const float* v, float scale) {
+template <bool F16>
+__device__ __forceinline__ void store_x8(uint16_t* p, const float* v, float scale) {
+  using E = NvkElt<F16>;
   nvk_u32x4 w;
-  w.x = nvk_pack_bf16x2(v[0] * scale, v[1] * scale);
-  w.y = nvk_pack_bf16x2(v[2] * scale, v[3] * scale);
-  w.z = nvk_pack_bf16x2(v[4] * scale, v[5] * scale);
-  w.w = nvk_pack_bf16x2(v[6] * scale, v[7] * scale);
+  w.x = E::pack2(v[0] * scale, v[1] * scale);
+  w.y = E::pack2(v[2] * scale, v[3] * scale);
+  w.z = E::pack2(v[4] * scale, v[5] * scale);
+  w.w = E::pack2(v[6] * scale, v[7] * scale);
   *reinterpret_cast<nvk_u32x4*>(p) = w;
 }
 
-template <int HD, int G, bool ALIGNED, bool FUSED>
+template <int HD, int G, bool ALIGNED, bool FUSED, bool F16>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
+  static_assert(!(FUSED && F16), "the fused prologue is built for bf16");
   using CB = ChunkBuf<HD, G>;
   constexpr int RPI = 64 / CB::LPR;           // head rows per load instruction
   constexpr int REC_HEAD = G * (HD + 4);      // floats per head in a record
@@ -503,7 +508,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     } else {
       load_chunk<HD, G, ALIGNED, FUSED>(a, cur, ctx, role, tpi, buf);
     }
-    compute_chunk<HD, G>(a, buf, cur.k * a.tc, ctx, tpi, role, st);
+    compute_chunk<HD, G, F16>(a, buf, cur.k * a.tc, ctx, tpi, role, st);
     const bool last = c + 1 == c1;
     const bool group_end = cur.k == cur.n - 1;
     if (group_end || last) {
@@ -515,7 +520,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
           for (int h = 0; h < G; ++h) {
             const float inv = st.l[h] > 0.f ? 1.f / st.l[h] : 0.f;
-            store_bf16x8(a.out + (int64_t)cur.b * a.out_stride_tok +
+            store_x8<F16>(a.out + (int64_t)cur.b * a.out_stride_tok +
                              (int64_t)(kvh * G + h) * a.out_stride_head + 8 * role.j,
                          st.o[h], inv);
           }
@@ -601,7 +606,7 @@ __device__ __forceinline__ float merge_parts(const DecodeArgs& a, const float* r
   return L > 0.f ? O / L : 0.f;
 }
 
-template <int HD, int G>
+template <int HD, int G, bool F16>
 __global__ __launch_bounds__(G * HD) void paged_decode_combine_kernel(DecodeArgs a) {
   constexpr int REC_HEAD = G * (HD + 4);  // floats per kv head in a record
   const int kvh = blockIdx.x, b = blockIdx.y;
@@ -621,7 +626,7 @@ __global__ __launch_bounds__(G * HD) void paged_decode_combine_kernel(DecodeArgs
   // round trip; the others 16 (uniform over the workgroup)
   const float r = p2 - p1 < 16 ? merge_parts<16, HD, G>(a, rec0, p1, p2, d)
                                : merge_parts<32, HD, G>(a, rec0, p1, p2, d);
-  *op = __builtin_bit_cast(uint16_t, (__bf16)r);
+  *op = NvkElt<F16>::one(r);
 }
 
 // kv heads per load instruction.  One: a group is then one (sequence, kv
@@ -660,27 +665,29 @@ size_t decode_ws_bytes(int batch, int num_q_heads, int num_kv_heads, int head_di
   return desc + P * 2 * hpi * G * (head_dim + 4) * sizeof(float);
 }
 
-template <int HD, int G, bool FUSED = false>
+template <int HD, int G, bool FUSED, bool F16>
 int launch_decode(const DecodeArgs& a, bool aligned, hipStream_t stream) {
   const dim3 grid(a.n_waves / kWavesPerWG);
   if (aligned)
-    hipLaunchKernelGGL((paged_decode_kernel<HD, G, true, FUSED>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((paged_decode_kernel<HD, G, true, FUSED, F16>), grid, dim3(256), 0, stream,
+                       a);
   else
-    hipLaunchKernelGGL((paged_decode_kernel<HD, G, false, FUSED>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((paged_decode_kernel<HD, G, false, FUSED, F16>), grid, dim3(256), 0,
+                       stream, a);
   int st = nvk_launch_status();
   if (st != NVK_OK) return st;
-  hipLaunchKernelGGL((paged_decode_combine_kernel<HD, G>), dim3(a.num_kv_heads, a.batch),
+  hipLaunchKernelGGL((paged_decode_combine_kernel<HD, G, F16>), dim3(a.num_kv_heads, a.batch),
                      dim3(G * HD), 0, stream, a);
   return nvk_launch_status();
 }
 
-template <int HD, bool FUSED = false>
+template <int HD, bool FUSED = false, bool F16 = false>
 int dispatch_group(const DecodeArgs& a, int G, bool aligned, hipStream_t s) {
   switch (G) {
-    case 1: return launch_decode<HD, 1, FUSED>(a, aligned, s);
-    case 2: return launch_decode<HD, 2, FUSED>(a, aligned, s);
-    case 4: return launch_decode<HD, 4, FUSED>(a, aligned, s);
-    case 8: return launch_decode<HD, 8, FUSED>(a, aligned, s);
+    case 1: return launch_decode<HD, 1, FUSED, F16>(a, aligned, s);
+    case 2: return launch_decode<HD, 2, FUSED, F16>(a, aligned, s);
+    case 4: return launch_decode<HD, 4, FUSED, F16>(a, aligned, s);
+    case 8: return launch_decode<HD, 8, FUSED, F16>(a, aligned, s);
     default: return NVK_EUNSUPPORTED;
   }
 }
@@ -699,7 +706,7 @@ int decode_setup(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
       num_blocks < 0)
     return NVK_EINVAL;
   if (!(scale > 0.f)) return NVK_EINVAL;
-  if (dtype != NVK_DTYPE_BF16) return NVK_EUNSUPPORTED;
+  if (dtype != NVK_DTYPE_BF16 && dtype != NVK_DTYPE_F16) return NVK_EUNSUPPORTED;
   if (num_q_heads % num_kv_heads) return NVK_EINVAL;
   if (head_dim != 64 && head_dim != 128) return NVK_EUNSUPPORTED;
   const int G = num_q_heads / num_kv_heads;
@@ -744,6 +751,7 @@ int decode_setup(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
   a.hpi = decode_hpi(num_kv_heads, head_dim);
   a.tc = tc;
   a.n_waves = decode_waves(batch, num_kv_heads, head_dim, block_size, max_blocks);
+  a.f16 = dtype == NVK_DTYPE_F16;
   return NVK_OK;
 }
 
@@ -754,6 +762,10 @@ int decode_run(DecodeArgs& a, int head_dim, void* workspace, hipStream_t s) {
   a.ws_rec = reinterpret_cast<float*>(static_cast<char*>(workspace) + desc);
   const bool aligned = (a.block_size % a.tc) == 0;
   const int G = a.num_q_heads / a.num_kv_heads;
+  if (a.f16) {
+    if (head_dim == 128) return dispatch_group<128, false, true>(a, G, aligned, s);
+    return dispatch_group<64, false, true>(a, G, aligned, s);
+  }
   if (head_dim == 128) return dispatch_group<128>(a, G, aligned, s);
   return dispatch_group<64>(a, G, aligned, s);
 }

@@ -22,6 +22,7 @@ struct ShortQueryParams {
   float scale;
   uint16_t* out;
   int64_t out_stride_tok, out_stride_head;
+  bool f16;  // elements are f16 (else bf16)
 };
 
 // True when the short-query kernels cover a launch of these sizes: paged keys

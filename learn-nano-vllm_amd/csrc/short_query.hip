@@ -139,7 +139,10 @@ __device__ __forceinline__ float max_xor16(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+template <bool F16>
 __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs a) {
+  using E = NvkElt<F16>;
+  typedef typename E::vec8 vec8;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kWavesPerWG * kChunkBytes];
   __shared__ int s_cs[kMaxBatch + 1];
   __shared__ int s_wsum[kWavesPerWG];
@@ -198,7 +201,7 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
   }
 
   // per-group state
-  nvk_bf16x8 qf[HD / 32];
+  vec8 qf[HD / 32];
   nvk_f32x4 acc_o[HD / 16];
   float m_run = -INFINITY, l_part = 0.f;
   int q_row0 = 0, Lq = 0, nkeys = 0, diag = 0, tok = 0, head = 0;
@@ -222,7 +225,7 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
     for (int ks = 0; ks < HD / 32; ++ks) {
       nvk_u32x4 v = {0u, 0u, 0u, 0u};
       if (row_valid) v = *reinterpret_cast<const nvk_u32x4*>(qp + 32 * ks);
-      qf[ks] = __builtin_bit_cast(nvk_bf16x8, v);
+      qf[ks] = __builtin_bit_cast(vec8, v);
     }
 #pragma unroll
     for (int db = 0; db < HD / 16; ++db) acc_o[db] = nvk_f32x4{0.f, 0.f, 0.f, 0.f};
@@ -257,14 +260,14 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
   // key 16 kb + r, and its k-step ks covers d = 32 ks + 8 g .. +7 (the head
   // dimension is permuted identically in Q, which leaves q . k unchanged), so
   // the four lanes of a key read 64 contiguous bytes per load.
-  auto issue_k = [&](const ChunkSrc& cs, int rem_rows, nvk_bf16x8 (&kf)[4][HD / 32]) {
+  auto issue_k = [&](const ChunkSrc& cs, int rem_rows, vec8 (&kf)[4][HD / 32]) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const bool ok = 16 * kb + r < rem_rows;
       const uint16_t* src = ok ? cs.k + (int64_t)16 * kb * a.row_elems : a.p.k_cache + 8 * g;
 #pragma unroll
       for (int ks = 0; ks < HD / 32; ++ks)
-        kf[kb][ks] = __builtin_bit_cast(nvk_bf16x8, *reinterpret_cast<const nvk_u32x4*>(src + 32 * ks));
+        kf[kb][ks] = __builtin_bit_cast(vec8, *reinterpret_cast<const nvk_u32x4*>(src + 32 * ks));
     }
   };
   auto issue_v = [&](const ChunkSrc& cs) {
@@ -280,7 +283,7 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
   };
 
   start_group();
-  nvk_bf16x8 kf[4][HD / 32];
+  vec8 kf[4][HD / 32];
   {
     const ChunkSrc cs = chunk_src(s, kvh, k, bt_row, nkeys);
     issue_k(cs, rows_of(k, bt_row, nkeys), kf);
@@ -298,7 +301,7 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
       sacc[kb] = nvk_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < HD / 32; ++ks)
-        sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb][ks], qf[ks], sacc[kb], 0, 0, 0);
+        sacc[kb] = E::mfma16x16x32(kf[kb][ks], qf[ks], sacc[kb]);
     }
 
     // ---- the next chunk's position; its K loads go out now (kf is free)
@@ -346,24 +349,24 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
     l_part *= alpha;
 #pragma unroll
     for (int db = 0; db < HD / 16; ++db) acc_o[db] *= alpha;
-    constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1, 1)
-    nvk_bf16x8 pf[2];
+    constexpr uint32_t kOnes = E::kOnes;  // the pair (1, 1)
+    vec8 pf[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       uint32_t wds[4];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const nvk_f32x4& sv = sacc[2 * p + h];
-        const uint32_t w0 = nvk_pack_bf16x2(nvk_fast_exp2(fmaf(sv[0], a.scale_log2, -moff)),
+        const uint32_t w0 = E::pack2(nvk_fast_exp2(fmaf(sv[0], a.scale_log2, -moff)),
                                             nvk_fast_exp2(fmaf(sv[1], a.scale_log2, -moff)));
-        const uint32_t w1 = nvk_pack_bf16x2(nvk_fast_exp2(fmaf(sv[2], a.scale_log2, -moff)),
+        const uint32_t w1 = E::pack2(nvk_fast_exp2(fmaf(sv[2], a.scale_log2, -moff)),
                                             nvk_fast_exp2(fmaf(sv[3], a.scale_log2, -moff)));
-        l_part = nvk_dot2_bf16(w0, kOnes, l_part);
-        l_part = nvk_dot2_bf16(w1, kOnes, l_part);
+        l_part = E::dot2(w0, kOnes, l_part);
+        l_part = E::dot2(w1, kOnes, l_part);
         wds[2 * h] = w0;
         wds[2 * h + 1] = w1;
       }
-      pf[p] = __builtin_bit_cast(nvk_bf16x8, nvk_u32x4{wds[0], wds[1], wds[2], wds[3]});
+      pf[p] = __builtin_bit_cast(vec8, nvk_u32x4{wds[0], wds[1], wds[2], wds[3]});
     }
     // ---- O^T += V^T P^T
 #pragma unroll
@@ -377,8 +380,7 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
         const nvk_i16x4 vhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) nvk_i16x4*)(size_t)a_hi);
         const nvk_i16x8 vv = {vlo[0], vlo[1], vlo[2], vlo[3], vhi[0], vhi[1], vhi[2], vhi[3]};
-        acc_o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(nvk_bf16x8, vv), pf[p],
-                                                             acc_o[db], 0, 0, 0);
+        acc_o[db] = E::mfma16x16x32(__builtin_bit_cast(vec8, vv), pf[p], acc_o[db]);
       }
     }
     // the V buffer is free again: the next chunk's V goes out
@@ -396,8 +398,8 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
 #pragma unroll
           for (int db = 0; db < HD / 16; ++db) {
             nvk_u32x2 wv;
-            wv.x = nvk_pack_bf16x2(acc_o[db][0] * inv, acc_o[db][1] * inv);
-            wv.y = nvk_pack_bf16x2(acc_o[db][2] * inv, acc_o[db][3] * inv);
+            wv.x = E::pack2(acc_o[db][0] * inv, acc_o[db][1] * inv);
+            wv.y = E::pack2(acc_o[db][2] * inv, acc_o[db][3] * inv);
             *reinterpret_cast<nvk_u32x2*>(op + 16 * db) = wv;
           }
         }
@@ -471,6 +473,7 @@ __device__ __forceinline__ void sq_merge_parts(const SqArgs& a, int row, int d0,
   }
 }
 
+template <bool F16>
 __global__ __launch_bounds__(512) void short_query_combine_kernel(SqArgs a) {
   const int kvh = blockIdx.x, s = blockIdx.y;
   const int row = threadIdx.x >> 5, d0 = 4 * (threadIdx.x & 31);
@@ -497,8 +500,8 @@ __global__ __launch_bounds__(512) void short_query_combine_kernel(SqArgs a) {
     sq_merge_parts<16>(a, row, d0, p1, p2, L, O);
   const float inv = L > 0.f ? 1.f / L : 0.f;
   nvk_u32x2 wv;
-  wv.x = nvk_pack_bf16x2(O[0] * inv, O[1] * inv);
-  wv.y = nvk_pack_bf16x2(O[2] * inv, O[3] * inv);
+  wv.x = NvkElt<F16>::pack2(O[0] * inv, O[1] * inv);
+  wv.y = NvkElt<F16>::pack2(O[2] * inv, O[3] * inv);
   *reinterpret_cast<nvk_u32x2*>(op) = wv;
 }
 
@@ -544,11 +547,19 @@ int short_query_launch(const ShortQueryParams& p, int64_t max_keys, void* ws, hi
   a.desc = static_cast<int32_t*>(ws);
   a.rec = reinterpret_cast<float*>(static_cast<char*>(ws) + sq_desc_bytes(p.batch, p.num_kv_heads));
   a.n_waves = sq_waves(p.batch, max_keys, p.num_kv_heads);
-  hipLaunchKernelGGL(short_query_kernel, dim3(a.n_waves / kWavesPerWG), dim3(64 * kWavesPerWG), 0, s,
-                     a);
+  if (p.f16)
+    hipLaunchKernelGGL(short_query_kernel<true>, dim3(a.n_waves / kWavesPerWG),
+                       dim3(64 * kWavesPerWG), 0, s, a);
+  else
+    hipLaunchKernelGGL(short_query_kernel<false>, dim3(a.n_waves / kWavesPerWG),
+                       dim3(64 * kWavesPerWG), 0, s, a);
   int st = nvk_launch_status();
   if (st != NVK_OK) return st;
-  hipLaunchKernelGGL(short_query_combine_kernel, dim3(p.num_kv_heads, p.batch), dim3(32 * kR), 0, s,
-                     a);
+  if (p.f16)
+    hipLaunchKernelGGL(short_query_combine_kernel<true>, dim3(p.num_kv_heads, p.batch),
+                       dim3(32 * kR), 0, s, a);
+  else
+    hipLaunchKernelGGL(short_query_combine_kernel<false>, dim3(p.num_kv_heads, p.batch),
+                       dim3(32 * kR), 0, s, a);
   return nvk_launch_status();
 }

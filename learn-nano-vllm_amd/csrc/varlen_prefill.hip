@@ -258,9 +258,11 @@ __device__ __forceinline__ void wait_lds_loads() {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <int G, int MODE>
+template <int G, int MODE, bool F16>
 __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel(PrefillArgs a) {
   constexpr int TQ = kRows / G;  // query tokens per workgroup
+  using E = NvkElt<F16>;
+  typedef typename E::vec8 vec8;
 
   const int kvh = blockIdx.x;
   int s = blockIdx.y, z = blockIdx.z;
@@ -306,7 +308,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
   const int tok = q0 + row / G;
   const int head = kvh * G + row % G;
   const bool row_valid = tok >= 0 && tok < Lq;
-  nvk_bf16x8 qf[HD / 16];
+  vec8 qf[HD / 16];
   {
     const int64_t qrow = (int64_t)q_row0 + tok;
     const bool ok = row_valid && qrow < a.total_q;
@@ -315,7 +317,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     for (int ks = 0; ks < HD / 16; ++ks) {
       nvk_u32x4 w = {0, 0, 0, 0};
       if (ok) w = *reinterpret_cast<const nvk_u32x4*>(qp + 16 * ks);
-      qf[ks] = __builtin_bit_cast(nvk_bf16x8, w);
+      qf[ks] = __builtin_bit_cast(vec8, w);
     }
   }
   const int row_limit = tok + diag;  // last visible key of this row
@@ -424,9 +426,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       const uint32_t addr = ka ^ (32u * ks);
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
-        const nvk_bf16x8 kf = *reinterpret_cast<const __attribute__((address_space(3)))
-                                                    nvk_bf16x8*>((size_t)(addr + 32 * kRowBytes * mb));
-        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], acc[mb], 0, 0, 0);
+        const vec8 kf = *reinterpret_cast<const __attribute__((address_space(3))) vec8*>(
+            (size_t)(addr + 32 * kRowBytes * mb));
+        acc[mb] = E::mfma32x32x16(kf, qf[ks], acc[mb]);
       }
     }
   };
@@ -503,12 +505,11 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
   // order): exp2(score * scale_log2 - moff) of two scores packed to bf16; the
   // row sum accumulates the same rounded values that enter the PV product.
   auto exp_word = [&](const nvk_f32x16 (&sc)[2], float moff, int p, int e) -> uint32_t {
-    constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 (1, 1)
     const int mb = p >> 1, i = 8 * (p & 1) + 2 * e;
     const float p0 = nvk_fast_exp2(fmaf(sc[mb][i], a.scale_log2, -moff));
     const float p1 = nvk_fast_exp2(fmaf(sc[mb][i + 1], a.scale_log2, -moff));
-    uint32_t w = nvk_pack_bf16x2(p0, p1);
-    l_part[e & 1] = nvk_dot2_bf16(w, kOnes, l_part[e & 1]);
+    uint32_t w = E::pack2(p0, p1);
+    l_part[e & 1] = E::dot2(w, E::kOnes, l_part[e & 1]);  // the pair (1, 1)
     // keep this word where it is placed among the MFMAs (no sinking to its use)
     asm volatile("" : "+v"(w), "+v"(l_part[e & 1]));
     return w;
@@ -535,7 +536,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     uint32_t va_lo = v_lo0 + (kt & 1) * kTileBytes, va_hi = v_hi0 + (kt & 1) * kTileBytes;
     asm volatile("" : "+v"(ka), "+v"(va_lo), "+v"(va_hi));  // rebuilt per step
     auto rd_k = [&](int ks, int mb) {
-      return *reinterpret_cast<const __attribute__((address_space(3))) nvk_bf16x8*>(
+      return *reinterpret_cast<const __attribute__((address_space(3))) vec8*>(
           (size_t)((ka ^ (32u * ks)) + 32 * kRowBytes * mb));
     };
     auto rd_v = [&](int db, int ks) {
@@ -546,10 +547,10 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
           (__attribute__((address_space(3))) nvk_i16x4*)(size_t)((va_hi ^ (64u * db)) +
                                                                   16 * ks * kRowBytes));
       const nvk_i16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      return __builtin_bit_cast(nvk_bf16x8, w);
+      return __builtin_bit_cast(vec8, w);
     };
     auto pack = [](const uint32_t (&w)[4]) {
-      return __builtin_bit_cast(nvk_bf16x8, nvk_u32x4{w[0], w[1], w[2], w[3]});
+      return __builtin_bit_cast(vec8, nvk_u32x4{w[0], w[1], w[2], w[3]});
     };
     // loads of this step: V(kt+1) during the O MFMAs, K(kt+2) during the S MFMAs
     auto v_load_at = [&](int idx) {  // O MFMA index -> load number or -1
@@ -564,9 +565,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
         if (kAt[kLoadsPerWave > 2 ? j : 2 * j] == i) return j;
       return -1;
     };
-    nvk_bf16x8 pf[4];
+    vec8 pf[4];
     uint32_t pw[4], pw3[4];
-    nvk_bf16x8 vf[3];
+    vec8 vf[3];
     vf[0] = rd_v(0, 0);
     vf[1] = rd_v(1, 0);
 #pragma unroll
@@ -578,7 +579,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       const int ks = idx / (HD / 32), db = idx % (HD / 32);
       if (idx + 2 < kO) vf[(idx + 2) % 3] = rd_v((idx + 2) % (HD / 32), (idx + 2) / (HD / 32));
       __builtin_amdgcn_sched_barrier(0);
-      acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[idx % 3], pf[ks], acc_o[db], 0, 0, 0);
+      acc_o[db] = E::mfma32x32x16(vf[idx % 3], pf[ks], acc_o[db]);
       const int j = v_load_at(idx);
       if (j >= 0) issue_load(plan_v, j, true);
     };
@@ -592,7 +593,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     pf[1] = pack(pw);
     // S(kt+1), block 0 then block 1.  After the last tile this multiplies a
     // stale (or zero-filled) K stage; the result is unused.
-    nvk_bf16x8 kf[3];
+    vec8 kf[3];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       kf[0] = rd_k(0, mb);
@@ -602,7 +603,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       for (int ks = 0; ks < HD / 16; ++ks) {
         if (ks + 2 < HD / 16) kf[(ks + 2) % 3] = rd_k(ks + 2, mb);
         __builtin_amdgcn_sched_barrier(0);
-        sc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks % 3], qf[ks], sc[mb], 0, 0, 0);
+        sc[mb] = E::mfma32x32x16(kf[ks % 3], qf[ks], sc[mb]);
         if (mb == 0) {
           if (ks < 4) pw[ks] = exp_word(sc, moff, 2, ks);
           else pw3[ks - 4] = exp_word(sc, moff, 3, ks - 4);
@@ -740,8 +741,8 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     for (int grp = 0; grp < 4; ++grp) {
       const int d = 32 * db + 8 * grp + 4 * half;
       nvk_u32x2 w;
-      w.x = nvk_pack_bf16x2(acc_o[db][4 * grp] * inv, acc_o[db][4 * grp + 1] * inv);
-      w.y = nvk_pack_bf16x2(acc_o[db][4 * grp + 2] * inv, acc_o[db][4 * grp + 3] * inv);
+      w.x = E::pack2(acc_o[db][4 * grp] * inv, acc_o[db][4 * grp + 1] * inv);
+      w.y = E::pack2(acc_o[db][4 * grp + 2] * inv, acc_o[db][4 * grp + 3] * inv);
       *reinterpret_cast<nvk_u32x2*>(op + d) = w;
     }
   }
@@ -749,7 +750,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
 
 // Merges the split-K partial records of one (sequence, kv head, query tile):
 // thread t handles row t/2 and d range 64*(t%2) .. +63.
-template <int G, int MODE>
+template <int G, int MODE, bool F16>
 __global__ __launch_bounds__(2 * kRows) void prefill_combine_kernel(PrefillArgs a) {
   constexpr int TQ = kRows / G;
   const int kvh = blockIdx.x, s = blockIdx.y, qt = blockIdx.z;
@@ -790,30 +791,42 @@ __global__ __launch_bounds__(2 * kRows) void prefill_combine_kernel(PrefillArgs 
 #pragma unroll
   for (int i = 0; i < 16; ++i) {  // 8-byte stores: out is only required 8-byte aligned
     nvk_u32x2 w;
-    w.x = nvk_pack_bf16x2(acc[i][0] * inv, acc[i][1] * inv);
-    w.y = nvk_pack_bf16x2(acc[i][2] * inv, acc[i][3] * inv);
+    w.x = NvkElt<F16>::pack2(acc[i][0] * inv, acc[i][1] * inv);
+    w.y = NvkElt<F16>::pack2(acc[i][2] * inv, acc[i][3] * inv);
     *reinterpret_cast<nvk_u32x2*>(op + 4 * i) = w;
   }
 }
 
-template <int G, int MODE>
+template <int G, int MODE, bool F16>
 int launch_mode(const PrefillArgs& a, hipStream_t stream) {
   dim3 grid(a.num_kv_heads, a.batch, a.n_qtiles * a.n_splits);
-  hipLaunchKernelGGL((varlen_prefill_kernel<G, MODE>), grid, dim3(64 * kWaves), 0, stream, a);
+  hipLaunchKernelGGL((varlen_prefill_kernel<G, MODE, F16>), grid, dim3(64 * kWaves), 0, stream,
+                     a);
   if (a.n_splits > 1) {
     const int st = nvk_launch_status();
     if (st != NVK_OK) return st;
     dim3 cgrid(a.num_kv_heads, a.batch, a.n_qtiles);
-    hipLaunchKernelGGL((prefill_combine_kernel<G, MODE>), cgrid, dim3(2 * kRows), 0, stream, a);
+    hipLaunchKernelGGL((prefill_combine_kernel<G, MODE, F16>), cgrid, dim3(2 * kRows), 0, stream,
+                       a);
   }
   return nvk_launch_status();
 }
 
-template <int G>
+template <int G, bool F16>
 int launch_prefill(const PrefillArgs& a, hipStream_t stream) {
-  if (!a.block_tables) return launch_mode<G, kDense>(a, stream);
-  if (a.block_size % kKeys == 0) return launch_mode<G, kPagedAligned>(a, stream);
-  return launch_mode<G, kPagedAny>(a, stream);
+  if (!a.block_tables) return launch_mode<G, kDense, F16>(a, stream);
+  if (a.block_size % kKeys == 0) return launch_mode<G, kPagedAligned, F16>(a, stream);
+  return launch_mode<G, kPagedAny, F16>(a, stream);
+}
+
+template <bool F16>
+int launch_prefill_g(const PrefillArgs& a, int G, hipStream_t s) {
+  switch (G) {
+    case 1: return launch_prefill<1, F16>(a, s);
+    case 2: return launch_prefill<2, F16>(a, s);
+    case 4: return launch_prefill<4, F16>(a, s);
+    default: return launch_prefill<8, F16>(a, s);
+  }
 }
 
 
@@ -911,7 +924,7 @@ int varlen_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_he
       num_kv_heads <= 0 || total_q < 0 || total_k < 0)
     return NVK_EINVAL;
   if (!(scale > 0.f)) return NVK_EINVAL;  // the row max is taken before scaling
-  if (dtype != NVK_DTYPE_BF16) return NVK_EUNSUPPORTED;
+  if (dtype != NVK_DTYPE_BF16 && dtype != NVK_DTYPE_F16) return NVK_EUNSUPPORTED;
   if (head_dim != HD) return NVK_EUNSUPPORTED;
   if (num_q_heads % num_kv_heads) return NVK_EINVAL;
   const int G = num_q_heads / num_kv_heads;
@@ -967,6 +980,7 @@ int varlen_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_he
     sp.out = static_cast<uint16_t*>(out);
     sp.out_stride_tok = out_stride_tok;
     sp.out_stride_head = out_stride_head;
+    sp.f16 = dtype == NVK_DTYPE_F16;
     return short_query_launch(sp, max_keys, workspace, reinterpret_cast<hipStream_t>(stream));
   }
   SplitPlan sp = plan_splits(batch, max_seqlen_q, max_keys, num_q_heads, num_kv_heads);
@@ -1025,12 +1039,7 @@ int varlen_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_he
       a.order = order;
     }
   }
-  switch (G) {
-    case 1: return launch_prefill<1>(a, s);
-    case 2: return launch_prefill<2>(a, s);
-    case 4: return launch_prefill<4>(a, s);
-    default: return launch_prefill<8>(a, s);
-  }
+  return dtype == NVK_DTYPE_F16 ? launch_prefill_g<true>(a, G, s) : launch_prefill_g<false>(a, G, s);
 }
 
 }  // namespace

@@ -21,10 +21,15 @@ def _unsupported(**opts) -> None:
             raise NotImplementedError(f"nanovllm_amd: {name}={value!r} is not supported")
 
 
-def _check_bf16(*ts: torch.Tensor) -> None:
-    for t in ts:
-        if t.dtype != torch.bfloat16:
-            raise _lib.NvkError(f"attention kernels are built for bfloat16, got {t.dtype}")
+def _attn_dtype(*ts: torch.Tensor) -> int:
+    """The library's code for the one 16-bit type (bf16 or fp16) of q, k, v."""
+    dt = ts[0].dtype
+    if dt not in (torch.bfloat16, torch.float16):
+        raise _lib.NvkError(f"attention kernels are built for bfloat16 and float16, got {dt}")
+    for t in ts[1:]:
+        if t.dtype != dt:
+            raise _lib.NvkError(f"q, k and v must share one dtype: {dt} and {t.dtype}")
+    return _lib.dtype_code(ts[0])
 
 
 def _int32(t: torch.Tensor) -> torch.Tensor:
@@ -77,7 +82,7 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_sc
     from prefill_tile_order with the same metadata (ranked once per step).
     """
     dev = _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, block_table)
-    _check_bf16(q, k, v)
+    dtype = _attn_dtype(q, k, v)
     if q.dim() != 3 or q.stride(-1) != 1:
         raise _lib.NvkError("q must be [tokens, heads, head_dim] with unit last stride")
     tq, hq, d = q.shape
@@ -126,7 +131,7 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_sc
             hq, hkv, d, scale,
             out.data_ptr(), out.stride(0), out.stride(1),
             _lib.ptr(ws), ws_bytes, _lib.ptr(order),
-            _lib.NVK_DTYPE_BF16, _lib.stream_ptr(dev))
+            dtype, _lib.stream_ptr(dev))
     _lib.check(code)
     return out
 
@@ -135,7 +140,7 @@ def paged_decode(q, k_cache, v_cache, context_lens, block_table, softmax_scale, 
     """One query per sequence over its paged cache.  q: [B, Hq, D] (any token /
     head strides).  Returns [B, Hq, D] (or fills ``out``)."""
     dev = _lib.require_gpu(q, k_cache, v_cache, context_lens, block_table)
-    _check_bf16(q, k_cache, v_cache)
+    dtype = _attn_dtype(q, k_cache, v_cache)
     if q.dim() != 3 or q.stride(-1) != 1:
         raise _lib.NvkError("q must be [batch, heads, head_dim] with unit last stride")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()) or k_cache.shape != v_cache.shape:
@@ -160,7 +165,7 @@ def paged_decode(q, k_cache, v_cache, context_lens, block_table, softmax_scale, 
             q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
             bt.data_ptr(), bt.stride(0), lens.data_ptr(), b, hq, hkv, d, block_size, max_blocks,
             num_blocks, scale, out.data_ptr(), out.stride(0), out.stride(1),
-            _lib.ptr(ws), ws_bytes, _lib.NVK_DTYPE_BF16, _lib.stream_ptr(dev))
+            _lib.ptr(ws), ws_bytes, dtype, _lib.stream_ptr(dev))
     _lib.check(code)
     return out
 

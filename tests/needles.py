@@ -54,7 +54,7 @@ class NeedleCase:
     would make visible if it were read)."""
 
     def __init__(self, seed, lens_q, lens_k, block_size=256, hq=16, hkv=8, d=128,
-                 device="cuda"):
+                 device="cuda", dtype=torch.bfloat16):
         assert all(lk >= 2 for lk in lens_k) and len(lens_q) == len(lens_k)
         self.lens_q, self.lens_k = list(lens_q), list(lens_k)
         self.bs, self.hq, self.hkv, self.d = block_size, hq, hkv, d
@@ -64,7 +64,7 @@ class NeedleCase:
         b = len(lens_k)
         cpu = torch.Generator().manual_seed(seed)
         gen = torch.Generator(device=self.device).manual_seed(seed)
-        bf = torch.bfloat16
+        bf = dtype
         cu_q = [0]
         for n in lens_q:
             cu_q.append(cu_q[-1] + n)
@@ -108,6 +108,7 @@ class NeedleCase:
         if block_size:
             lk_t = torch.tensor(lens_k, device=self.device)[:, None].expand(b, hkv)
             kf[self.slots(lk_t), self.heads] = (4 * A * self.u).to(bf)[None]
+        self.dtype = bf
 
     def slots(self, pos: torch.Tensor) -> torch.Tensor:
         """Row of key pos[s, h] of sequence s in the flat [rows, Hkv, D] view."""
@@ -123,7 +124,7 @@ class NeedleCase:
         kf = self.k.view(-1, self.hkv, self.d)
         sl = self.slots(pos)
         saved = kf[sl, self.heads].clone()
-        kf[sl, self.heads] = (2 * A * self.u).to(torch.bfloat16)[None]
+        kf[sl, self.heads] = (2 * A * self.u).to(self.dtype)[None]
         return sl, saved
 
     def restore(self, planted) -> None:
@@ -156,7 +157,7 @@ class NeedleCase:
 def mismatches(out: torch.Tensor, exp: torch.Tensor) -> torch.Tensor:
     """Per row and head: 1 where out differs from exp by more than one bf16
     ulp (the expected rows are exact; the ulp covers the < 1e-12 relative
-    contribution of every other key)."""
+    contribution of every other key; an f16 ulp is smaller still)."""
     o, e = out.float(), exp.float()
     bad = (o - e).abs() > e.abs() * 2.0 ** -8 + 1e-6
     return bad.any(dim=-1)

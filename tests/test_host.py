@@ -46,10 +46,11 @@ def test_error_codes_without_launching():
     assert lib.nvk_kv_store(1, 8, 1, 8, 1, 1, 1, 4, 8, 3, 100, None) == -2
     assert lib.nvk_kv_store(1, 8, 1, 8, 1, 1, 1, -1, 8, 2, 100, None) == -1
     assert lib.nvk_kv_store(None, 8, None, 8, None, None, None, 0, 8, 2, 100, None) == 0
-    # decode: fp16 not built, head_dim 96 not built, G=3 not built, bad scale
+    # decode: f32 not built (bf16 and fp16 are), head_dim 96 not built, G=3 not
+    # built, bad scale
     args = [16, 16 * 128, 128, 16, 16, 16, 8, 16, 4, 16, 8, 128, 256, 8, 1024, 0.088, 16, 16 * 128,
             128, 16, 1 << 30]
-    assert lib.nvk_paged_decode(*args, 1, None) == -2
+    assert lib.nvk_paged_decode(*args, 2, None) == -2
     bad_hd = list(args); bad_hd[11] = 96
     assert lib.nvk_paged_decode(*bad_hd, 0, None) == -2
     bad_g = list(args); bad_g[9] = 12; bad_g[10] = 4
@@ -70,7 +71,7 @@ def test_error_codes_without_launching():
     # the no-allocation decode: the same argument checks, and sizes whose
     # workspace exceeds its 20 MiB static scratch rejected before any launch
     assert lib.nvk_strerror(-5).startswith(b"nvk:")
-    assert lib.nvk_paged_decode_noalloc(*args[:19], 1, None) == -2          # fp16
+    assert lib.nvk_paged_decode_noalloc(*args[:19], 2, None) == -2          # f32
     assert lib.nvk_paged_decode_noalloc(*bad_scale[:19], 0, None) == -1
     huge = list(args); huge[8], huge[9], huge[10] = 2048, 8192, 1024
     assert lib.nvk_paged_decode_workspace_size(2048, 8192, 1024, 128, 256, 8) > 20 << 20
