@@ -588,16 +588,20 @@ __device__ __forceinline__ float merge_parts(const DecodeArgs& a, const float* r
       ov[u] = rec[d];
       if (!ok) mv[u] = -INFINITY;
     }
+    // All 3 kBatch loads of the batch are issued before the fold starts (one
+    // round trip per batch): without the fence the compiler interleaves the
+    // running max with the loads and waits for each part in turn.
+    __builtin_amdgcn_sched_barrier(0);
     float mb = M;
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) mb = fmaxf(mb, mv[u]);
-    if (mb == -INFINITY) continue;
-    const float r = nvk_fast_exp2(M - mb);  // 0 while M is still -inf
+    const float mref = mb == -INFINITY ? 0.f : mb;  // no part so far: every weight 0
+    const float r = nvk_fast_exp2(M - mref);        // 0 while M is still -inf
     L *= r;
     O *= r;
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const float wt = nvk_fast_exp2(mv[u] - mb);
+      const float wt = nvk_fast_exp2(mv[u] - mref);
       L += lv[u] * wt;
       O += ov[u] * wt;
     }
