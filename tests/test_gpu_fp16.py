@@ -1,6 +1,6 @@
 """float16 attention on the GPU.  The reference runs attention in the model's
 dtype (nanovllm/engine/model_runner.py:29 sets torch's default dtype from
-hf_config.torch_dtype) and flash-attn takes bf16 and fp16 alike, so the
+hf_config.dtype) and flash-attn takes bf16 and fp16 alike, so the
 decode, varlen prefill (paged, dense, split-K, short-query) and KV-store
 accept fp16 tensors too: against the oracle within 2e-2 abs / 1e-2 rel, the
 store bit for bit, and the closed-form needle checks, which must hold exactly.
