@@ -305,13 +305,13 @@ def collect_traffic(run_root, out_path):
     print(json.dumps({k: v["bytes_per_launch"] for k, v in legs.items()}), flush=True)
 
 
-def mixed_leg(torch, dev, args, orc, cpu_jobs, layers=28):
+def mixed_leg(torch, dev, args, cpu_jobs, layers=28):
     """28 layers of one mixed step, each with its own KV pool (random bf16 made on
     the GPU) and the same block tables / slots; a layer = KV-store of every new
     token, the prefill chunks, the decodes."""
     from nanovllm_amd import paged_decode, store_kvcache, varlen_prefill
     from nanovllm_amd.flash_api import prefill_tile_order
-    from nanovllm_amd.workloads import mixed_step_metadata
+    from nanovllm_amd.workloads import attention_bytes, mixed_step_metadata, prefill_flops
 
     log(f"building mixed step ({layers} layers, ~3.5 GB of KV pool per layer)")
     tens, meta = mixed_step_metadata()
@@ -349,8 +349,8 @@ def mixed_leg(torch, dev, args, orc, cpu_jobs, layers=28):
     steps, warm = min(args.steps, 10), min(args.warmup, 2)
     log("timing mixed step")
     wall, ev = time_graph(torch, [step], steps, warm, args.eager)
-    dec_bytes = orc.attention_bytes(meta["dec_lens"], 8, 128, 192, 16)
-    pf_flops = orc.prefill_flops(meta["lens_q"], meta["lens_k"], 16, 128)
+    dec_bytes = attention_bytes(meta["dec_lens"], 8, 128, 192, 16)
+    pf_flops = prefill_flops(meta["lens_q"], meta["lens_k"], 16, 128)
     st_bytes = int((tens["slot_mapping"] >= 0).sum()) * 2 * 2 * 2048 + 4 * n_tok
     t_roof = layers * ((dec_bytes + st_bytes) / (HBM_PEAK_GBS * 1e9) +
                        pf_flops / (BF16_PEAK_TFLOPS * 1e12))
@@ -397,20 +397,20 @@ def mixed_cpu_baseline(torch, layers):
                       f"{layers}"}
 
 
-def prologue_leg(torch, dev, args, orc, cpu_jobs):
+def prologue_leg(torch, dev, args, cpu_jobs):
     """Fused q/k RMSNorm + RoPE + KV-store over the mixed step's 4288 new tokens
     of one layer (rotated copies of the inputs storing into one 3300-page pool), and the
     same steps as separate eager torch operations (the reference's
     layernorm.py:16-26 / rotary_embedding.py:6-14 code, then the store) for
     comparison."""
     from nanovllm_amd import qk_norm_rope_store, store_kvcache
-    from nanovllm_amd.workloads import prologue_case
+    from nanovllm_amd.workloads import prologue_bytes, prologue_case
 
     log("building prologue workload (4288 tokens of the mixed step, 3300-page pool)")
     pc = prologue_case()
     hq, hkv, hd, eps = pc.hq, pc.hkv, pc.hd, pc.eps
     n_valid = int((pc.slot_mapping >= 0).sum())
-    pbytes = orc.prologue_bytes(pc.n_tokens, n_valid, pc.n_unique_positions, hq, hkv, hd,
+    pbytes = prologue_bytes(pc.n_tokens, n_valid, pc.n_unique_positions, hq, hkv, hd,
                                 write_k=False)
     # copies of the step's inputs; every copy stores into other rows of one
     # shared pool (its slots shifted by a multiple of 53 pages, mod the pool)
@@ -484,7 +484,7 @@ def prologue_leg(torch, dev, args, orc, cpu_jobs):
     return leg
 
 
-def decode_graph_leg(torch, dev, args, orc, layers=28):
+def decode_graph_leg(torch, dev, args, layers=28):
     """The decode attention path of a 28-layer Qwen3-0.6B stack, captured per
     batch bucket and replayed as the reference's run_model does: per layer the
     fused prologue (q/k norms, rotation, store of the new token) and the paged
@@ -497,7 +497,7 @@ def decode_graph_leg(torch, dev, args, orc, layers=28):
     would write them inside the graph) and as the same step launched eagerly."""
     from nanovllm_amd.engine.graph_runner import DecodeGraphRunner
     from nanovllm_amd.utils.context import reset_context, set_context
-    from nanovllm_amd.workloads import decode_case, decode_stack
+    from nanovllm_amd.workloads import attention_bytes, decode_case, decode_stack, prologue_bytes
 
     dc = decode_case()
     b, nb, w = 64, dc.k_cache.shape[0], dc.block_tables.shape[1]
@@ -541,8 +541,8 @@ def decode_graph_leg(torch, dev, args, orc, layers=28):
     log("timing graph replays and eager launches, B = 64 and B = 4")
     t_graph, t_eager = timed(b)
     t_graph4, t_eager4 = timed(4)
-    per_layer = (orc.attention_bytes(dc.lens, 8, 128, b, 16) +
-                 orc.prologue_bytes(b, b, b, 16, 8, 128, write_k=False))
+    per_layer = (attention_bytes(dc.lens, 8, 128, b, 16) +
+                 prologue_bytes(b, b, b, 16, 8, 128, write_k=False))
     total = layers * per_layer
     del runner, stack, kv_cache
     return dict(ms_per_step=round(t_graph * 1e3, 4), eager_ms_per_step=round(t_eager * 1e3, 4),
@@ -558,16 +558,36 @@ def decode_graph_leg(torch, dev, args, orc, layers=28):
                           "frac": round(total / t_graph / 1e9 / HBM_PEAK_GBS, 4)})
 
 
-def metadata_leg(torch, dev, args):
-    """Step metadata built by the reference's host loops (restated in
-    engine/metadata.py) against the device builders, wall time per call
-    including the upload and a device synchronisation: a chunked-prefill step
-    of 64 sequences (U{0..1536} cached + U{100..1024} new tokens) and a
-    512-sequence decode step over U{256..4096}."""
+class _SeqRecord:
+    """The fields of a scheduled sequence that the step-metadata builders read
+    (the reference's Sequence carries them, nanovllm/engine/sequence.py)."""
+
+    def __init__(self, token_ids, block_table, num_cached_tokens=0, num_scheduled_tokens=0):
+        self.token_ids = token_ids
+        self.block_table = block_table
+        self.num_cached_tokens = num_cached_tokens
+        self.num_scheduled_tokens = num_scheduled_tokens
+
+    def __len__(self):
+        return len(self.token_ids)
+
+    def __getitem__(self, key):
+        return self.token_ids[key]
+
+    @property
+    def last_token(self):
+        return self.token_ids[-1]
+
+
+def metadata_leg(torch, dev, args, cpu_jobs):
+    """Step metadata built by the device builders, wall time per call including
+    the upload and a device synchronisation: a chunked-prefill step of 64
+    sequences (U{0..1536} cached + U{100..1024} new tokens) and a 512-sequence
+    decode step over U{256..4096}.  The CPU baseline runs the reference's host
+    loops (restated in oracle/step_metadata.py) on the same sequences, with the
+    same upload and synchronisation."""
     import random
-    from nanovllm_amd.engine import metadata
     from nanovllm_amd.engine.device_metadata import prepare_decode_device, prepare_prefill_device
-    from nanovllm_amd.engine.sequence import Sequence
     from nanovllm_amd.utils.context import reset_context
 
     rng = random.Random(8)
@@ -579,16 +599,16 @@ def metadata_leg(torch, dev, args):
     for _ in range(64):
         c, m = rng.randint(0, 1536), rng.randint(100, 1024)
         need = (c + m + bs - 1) // bs
-        pf.append(Sequence([rng.randint(0, 150000) for _ in range(c + m)],
-                           block_table=pages[nxt:nxt + need], num_cached_tokens=c,
-                           num_scheduled_tokens=m))
+        pf.append(_SeqRecord([rng.randint(0, 150000) for _ in range(c + m)],
+                             block_table=pages[nxt:nxt + need], num_cached_tokens=c,
+                             num_scheduled_tokens=m))
         nxt += need
     dc = []
     for _ in range(512):
         n = rng.randint(256, 4096)
         need = (n + bs - 1) // bs
-        dc.append(Sequence([rng.randint(0, 150000) for _ in range(n)],
-                           block_table=pages[nxt:nxt + need]))
+        dc.append(_SeqRecord([rng.randint(0, 150000) for _ in range(n)],
+                             block_table=pages[nxt:nxt + need]))
         nxt += need
 
     def wall(fn, reps):
@@ -604,20 +624,35 @@ def metadata_leg(torch, dev, args):
             reset_context()
         return statistics.median(ts)
 
-    log("timing step metadata builders (host loops vs device kernel)")
+    log("timing step metadata builders (device kernels)")
     reps = 20
     res = {
         "prefill_64_seqs": {
             "tokens": sum(q.num_scheduled_tokens for q in pf),
-            "host_loops_ms": round(wall(lambda: metadata.prepare_prefill(pf, bs, dev), reps) * 1e3, 3),
             "device_ms": round(wall(lambda: prepare_prefill_device(pf, bs, dev), reps) * 1e3, 3)},
         "decode_512_seqs": {
-            "host_loops_ms": round(wall(lambda: metadata.prepare_decode(dc, bs, dev), reps) * 1e3, 3),
             "device_ms": round(wall(lambda: prepare_decode_device(dc, bs, dev), reps) * 1e3, 3)},
     }
     res["workload"] = ("slot_mapping / positions / cu_seqlens / padded block tables of a "
                        "64-sequence chunked prefill and a 512-sequence decode, median of "
                        f"{reps} calls, wall time with the device synchronised")
+    if not args.no_cpu_baseline:
+        def metadata_cpu():
+            from oracle import step_metadata as host
+            from oracle.sequence import Sequence
+            log("cpu baseline: step metadata by the reference's host loops")
+            pf_h = [Sequence(s.token_ids, s.block_table, s.num_cached_tokens,
+                             s.num_scheduled_tokens) for s in pf]
+            dc_h = [Sequence(s.token_ids, s.block_table) for s in dc]
+            return {"prefill_64_seqs_ms": round(wall(lambda: host.prepare_prefill(pf_h, bs, dev),
+                                                     reps) * 1e3, 3),
+                    "decode_512_seqs_ms": round(wall(lambda: host.prepare_decode(dc_h, bs, dev),
+                                                     reps) * 1e3, 3),
+                    "unit": "ms/call", "cores": 1, "kind": "port",
+                    "sample": "the same two steps through the reference's per-token host loops "
+                              "(one Python thread), upload and device synchronisation included, "
+                              f"median of {reps} calls"}
+        cpu_jobs.append(("step_metadata", metadata_cpu))
     return res
 
 
@@ -697,10 +732,9 @@ def main():
         return
 
     from nanovllm_amd import paged_decode, store_kvcache, varlen_prefill
-    from nanovllm_amd.workloads import (decode_case, kv_store_case, prefill_case,
+    from nanovllm_amd.workloads import (attention_bytes, decode_case, kv_store_case,
+                                        prefill_case, prefill_flops,
                                         spec_verify_case)
-    from oracle import kv_oracle as orc
-    from oracle import torch_cpu as tcpu
 
     legs = set(args.legs.split(","))
     dev = torch.device("cuda:0")
@@ -716,7 +750,7 @@ def main():
     # ------------------------------------------------------------------ decode
     log("building decode workload (B=64, ctx U{100..2048}, 1024-page pool)")
     dc = decode_case()
-    dec_bytes = orc.attention_bytes(dc.lens, 8, 128, 64, 16)
+    dec_bytes = attention_bytes(dc.lens, 8, 128, 64, 16)
     pools = [dc.to(dev) for _ in range(rotation(dec_bytes))]   # separate copies of the pool
     outs = [torch.empty(64, 16, 128, dtype=torch.bfloat16, device=dev) for _ in pools]
     dec_fns = [
@@ -730,6 +764,7 @@ def main():
     del pools, outs, dec_fns
     if not args.no_cpu_baseline:
         def decode_cpu():
+            from oracle import torch_cpu as tcpu
             threads = host_threads(torch)
             log(f"cpu baseline: decode on the PyTorch CPU path, {threads} threads")
             t = cpu_time(lambda: tcpu.paged_attention_cpu(dc.q, dc.k_cache, dc.v_cache, range(65),
@@ -770,6 +805,7 @@ def main():
                                   "bytes (and 512 MiB), same rotation, GB/s of read + write"})
         if not args.no_cpu_baseline:
             def store_cpu():
+                from oracle import torch_cpu as tcpu
                 threads = host_threads(torch)
                 log(f"cpu baseline: kv-store on the PyTorch CPU path, {threads} threads")
                 kc, vc = sc.k_cache.clone(), sc.v_cache.clone()
@@ -784,13 +820,13 @@ def main():
 
     # ------------------------------------------------------------------ prologue
     if "prologue" in legs:
-        result["prologue"] = prologue_leg(torch, dev, args, orc, cpu_jobs)
+        result["prologue"] = prologue_leg(torch, dev, args, cpu_jobs)
 
     # ------------------------------------------------------------------ prefill
     if "prefill" in legs:
         log("building prefill workload (32 seqs, 512-token shared prefix)")
         pc = prefill_case()
-        touched = orc.attention_bytes(pc.lens_k, 8, 128, sum(pc.lens_q), 16)
+        touched = attention_bytes(pc.lens_k, 8, 128, sum(pc.lens_q), 16)
         copies = [pc.to(dev) for _ in range(rotation(touched))]
         for c in copies:   # the new tokens' K/V are in the cache before attention
             store_kvcache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping)
@@ -799,7 +835,7 @@ def main():
                                                    c.cu_seqlens_k, pc.max_seqlen_q, pc.scale,
                                                    block_table=c.block_tables, out=o))
                   for c, o in zip(copies, outs)]
-        flops = orc.prefill_flops(pc.lens_q, pc.lens_k, 16, 128)
+        flops = prefill_flops(pc.lens_q, pc.lens_k, 16, 128)
         log("timing prefill")
         wall_p, ev_p = time_graph(torch, pf_fns, args.steps, args.warmup, args.eager)
         tf = flops / ev_p / 1e12
@@ -811,6 +847,7 @@ def main():
         del copies, outs, pf_fns
         if not args.no_cpu_baseline:
             def prefill_cpu():
+                from oracle import torch_cpu as tcpu
                 threads = host_threads(torch)
                 log(f"cpu baseline: prefill on the PyTorch CPU path, {threads} threads")
                 kc, vc = pc.k_cache.clone(), pc.v_cache.clone()
@@ -830,7 +867,7 @@ def main():
     if "spec" in legs:
         log("building spec-verify workload (32 seqs, 6 queries, ctx U{1024..8192})")
         vc_ = spec_verify_case()
-        sv_bytes = orc.attention_bytes(vc_.lens_k, 8, 128, 32 * 6, 16)
+        sv_bytes = attention_bytes(vc_.lens_k, 8, 128, 32 * 6, 16)
         copies = [vc_.to(dev) for _ in range(rotation(sv_bytes))]
         for c in copies:   # the 5 draft tokens of every sequence are stored first
             store_kvcache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping)
@@ -853,6 +890,7 @@ def main():
         del copies, outs, sv_fns
         if not args.no_cpu_baseline:
             def spec_cpu():
+                from oracle import torch_cpu as tcpu
                 threads = host_threads(torch)
                 log(f"cpu baseline: spec verify on the PyTorch CPU path, {threads} threads")
                 kc, vc = vc_.k_cache.clone(), vc_.v_cache.clone()
@@ -870,11 +908,11 @@ def main():
 
     # ------------------------------------------------------------------ decode graphs
     if "graph" in legs:
-        result["decode_graph"] = decode_graph_leg(torch, dev, args, orc)
+        result["decode_graph"] = decode_graph_leg(torch, dev, args)
 
     # ------------------------------------------------------------------ step metadata
     if "metadata" in legs:
-        result["step_metadata"] = metadata_leg(torch, dev, args)
+        result["step_metadata"] = metadata_leg(torch, dev, args, cpu_jobs)
 
     # ------------------------------------------------------------------ sampler
     if "sampler" in legs:
@@ -882,7 +920,7 @@ def main():
 
     # ------------------------------------------------------------------ mixed step
     if "mixed" in legs:
-        result["mixed_step"] = mixed_leg(torch, dev, args, orc, cpu_jobs)
+        result["mixed_step"] = mixed_leg(torch, dev, args, cpu_jobs)
 
     # ------------------------------------------------------------------ CPU baselines
     torch.cuda.synchronize()

@@ -1,1 +1,1 @@
-"""Host-side metadata builders of the KV-cache path (mirror of nanovllm/engine)."""
+"""Step metadata on the device and the bucketed decode-graph runner (the parts of nanovllm/engine that the KV-cache path needs)."""

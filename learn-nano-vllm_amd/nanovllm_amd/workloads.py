@@ -304,3 +304,40 @@ def decode_stack(num_layers, num_blocks, device, seed=6, hq=HQ, hkv=HKV, hd=HD,
         return torch.stack(outs, dim=1)
 
     return layers, rope, kv_cache, step
+
+
+# ---------------------------------------------------------------------------
+# Algorithmic work of a call (the numerators of the rooflines)
+# ---------------------------------------------------------------------------
+def attention_bytes(seqlens_k, num_kv_heads: int, head_dim: int, n_q_rows: int, num_q_heads: int,
+                    elem_bytes: int = 2) -> int:
+    """Unique K+V bytes of every sequence's keys + q read + out written."""
+    kv = 2 * sum(int(n) for n in seqlens_k) * num_kv_heads * head_dim * elem_bytes
+    return kv + 2 * n_q_rows * num_q_heads * head_dim * elem_bytes
+
+
+def prefill_flops(seqlens_q, seqlens_k, num_q_heads: int, head_dim: int) -> int:
+    """4 * Hq * D * (number of unmasked (query, key) pairs): QK^T plus PV.
+    Query row i of a sequence with Lq queries and Lk keys sees
+    min(Lk, i + Lk - Lq + 1) keys (bottom-right aligned causal mask)."""
+    pairs = 0
+    for lq, lk in zip(seqlens_q, seqlens_k):
+        lq, lk = int(lq), int(lk)
+        diag = lk - lq
+        for i in range(lq):
+            pairs += max(0, min(lk, i + diag + 1))
+    return 4 * num_q_heads * head_dim * pairs
+
+
+def prologue_bytes(n_tokens: int, n_valid_slots: int, n_unique_positions: int,
+                   num_q_heads: int, num_kv_heads: int, head_dim: int, write_k: bool) -> int:
+    """HBM bytes the fused prologue must move: the qkv rows, positions and
+    slots read, one cos/sin row per distinct position, q written, k and v
+    rows written to the caches for valid slots (and k written out if asked)."""
+    row = head_dim * 2
+    rd = n_tokens * (num_q_heads + 2 * num_kv_heads) * row + n_tokens * (8 + 4)
+    rd += n_unique_positions * head_dim * 4
+    wr = n_tokens * num_q_heads * row + n_valid_slots * 2 * num_kv_heads * row
+    if write_k:
+        wr += n_tokens * num_kv_heads * row
+    return rd + wr

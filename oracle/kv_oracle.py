@@ -69,8 +69,8 @@ from __future__ import annotations
 import numpy as np
 
 __all__ = ["bf16_to_f32", "f32_to_bf16", "kv_store", "slots_for", "gather_rows",
-           "paged_attention", "attention_bytes", "prefill_flops", "rms_norm",
-           "apply_rotary_emb", "qk_norm_rope_store", "prologue_bytes", "last_token_rows",
+           "paged_attention", "rms_norm",
+           "apply_rotary_emb", "qk_norm_rope_store", "last_token_rows",
            "sample_tokens"]
 
 
@@ -270,20 +270,6 @@ def qk_norm_rope_store(qkv_bits: np.ndarray, positions, q_weight_bits: np.ndarra
     return q, k, v
 
 
-def prologue_bytes(n_tokens: int, n_valid_slots: int, n_unique_positions: int,
-                   num_q_heads: int, num_kv_heads: int, head_dim: int, write_k: bool) -> int:
-    """HBM bytes the fused prologue must move: the qkv rows, positions and
-    slots read, one cos/sin row per distinct position, q written, k and v
-    rows written to the caches for valid slots (and k written out if asked)."""
-    row = head_dim * 2
-    rd = n_tokens * (num_q_heads + 2 * num_kv_heads) * row + n_tokens * (8 + 4)
-    rd += n_unique_positions * head_dim * 4
-    wr = n_tokens * num_q_heads * row + n_valid_slots * 2 * num_kv_heads * row
-    if write_k:
-        wr += n_tokens * num_kv_heads * row
-    return rd + wr
-
-
 # ---------------------------------------------------------------------------
 # LM-head last-token selection and the sampler
 # ---------------------------------------------------------------------------
@@ -307,24 +293,3 @@ def sample_tokens(logits: np.ndarray, temperatures, noise: np.ndarray,
     e = np.maximum(np.asarray(noise, dtype=np.float32), np.float32(1e-10))
     q = p * e if _mutation == "noise_mul" else p / e
     return np.argmax(q, axis=1).astype(np.int64)
-
-
-# ---------------------------------------------------------------------------
-# Algorithmic work counts (roofline numerators)
-# ---------------------------------------------------------------------------
-def attention_bytes(seqlens_k, num_kv_heads: int, head_dim: int, n_q_rows: int, num_q_heads: int,
-                    elem_bytes: int = 2) -> int:
-    """Unique K+V bytes of every sequence's keys + q read + out written."""
-    kv = 2 * int(np.sum(np.asarray(seqlens_k, dtype=np.int64))) * num_kv_heads * head_dim * elem_bytes
-    return kv + 2 * n_q_rows * num_q_heads * head_dim * elem_bytes
-
-
-def prefill_flops(seqlens_q, seqlens_k, num_q_heads: int, head_dim: int) -> int:
-    """4 * Hq * D * (number of unmasked (query, key) pairs): QK^T plus PV."""
-    pairs = 0
-    for lq, lk in zip(seqlens_q, seqlens_k):
-        lq, lk = int(lq), int(lk)
-        diag = lk - lq
-        for i in range(lq):
-            pairs += max(0, min(lk, i + diag + 1))
-    return 4 * num_q_heads * head_dim * pairs

@@ -1,5 +1,9 @@
 """Token-sequence record with the block arithmetic the metadata builders use.
 
+TEST INFRASTRUCTURE ONLY (see oracle/step_metadata.py): the input record of
+the metadata tests.  The device builders take any object with these fields,
+e.g. the reference's own Sequence.
+
 Mirrors the fields and properties of nanovllm/engine/sequence.py:14-65 that
 the KV-cache path reads: the token list, ``num_cached_tokens`` /
 ``num_scheduled_tokens`` (chunked prefill), the page list ``block_table`` and

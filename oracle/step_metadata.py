@@ -1,4 +1,9 @@
-"""Host-side builders of the attention metadata (the kernels' input contract).
+"""Host restatement of the reference's attention-metadata builders.
+
+TEST INFRASTRUCTURE ONLY, like the rest of oracle/: tests/ and the
+cpu_baseline leg of bench.py use it as the checker of the device builders
+(nanovllm_amd/engine/device_metadata.py) and as the timed host path; the
+product never imports it.
 
 Same outputs, dtypes and conventions as ModelRunner.prepare_block_tables /
 prepare_prefill / prepare_decode (nanovllm/engine/model_runner.py:123-188)

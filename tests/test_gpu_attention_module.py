@@ -14,8 +14,8 @@ import torch
 from gpu_utils import assert_attn_close, f32, say
 from oracle import kv_oracle as orc
 from nanovllm_amd import Attention
-from nanovllm_amd.engine import metadata
-from nanovllm_amd.engine.sequence import Sequence
+from oracle import step_metadata as metadata
+from oracle.sequence import Sequence
 from nanovllm_amd.utils.context import get_context, reset_context
 
 pytestmark = pytest.mark.gpu

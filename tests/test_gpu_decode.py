@@ -118,7 +118,7 @@ def test_decode_graph_capture_replays_with_padded_rows():
     # Capture store + decode once at batch 8 with all-zero metadata (as
     # capture_cudagraph does), then replay with live rows and padded rows.
     from nanovllm_amd import store_kvcache
-    from nanovllm_amd.engine.metadata import DecodeGraphBuffers
+    from oracle.step_metadata import DecodeGraphBuffers
     bs_graph, width = 8, 8
     pool = decode_case(seed=14, ctx=[1] * 8, pool_blocks=64)
     k_cache, v_cache = pool.k_cache.cuda(), pool.v_cache.cuda()

@@ -6,9 +6,9 @@ import random
 import pytest
 import torch
 
-from nanovllm_amd.engine import metadata
+from oracle import step_metadata as metadata
 from nanovllm_amd.engine.device_metadata import prepare_decode_device, prepare_prefill_device
-from nanovllm_amd.engine.sequence import Sequence
+from oracle.sequence import Sequence
 from nanovllm_amd.utils.context import get_context, reset_context
 from tests.gpu_utils import say
 

@@ -9,8 +9,8 @@ import pytest
 import torch
 
 from nanovllm_amd import _lib
-from nanovllm_amd.engine import metadata
-from nanovllm_amd.engine.sequence import Sequence
+from oracle import step_metadata as metadata
+from oracle.sequence import Sequence
 from nanovllm_amd.utils import context as ctx_mod
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -260,3 +260,19 @@ def test_pack_block_tables_is_the_compressed_table():
     seqs = [Sequence([1, 2, 3], block_table=[4, 5]), Sequence([1], block_table=[]),
             Sequence([1] * 9, block_table=[7, 8, 9])]
     assert pack_block_tables(seqs) == ([0, 2, 2, 5], [4, 5, 7, 8, 9], 3)
+
+
+def test_work_counts():
+    from nanovllm_amd.workloads import attention_bytes, prefill_flops, prologue_bytes
+    assert prefill_flops([2], [2], 1, 1) == 4 * 3
+    assert prefill_flops([1], [5], 2, 4) == 4 * 2 * 4 * 5
+    # brute force over the bottom-right causal mask, ragged and empty sequences
+    lq, lk = [3, 0, 7, 5], [10, 4, 7, 5]
+    pairs = sum(1 for q, k in zip(lq, lk) for i in range(q) for j in range(k) if j <= i + k - q)
+    assert prefill_flops(lq, lk, 3, 8) == 4 * 3 * 8 * pairs
+    assert attention_bytes([3, 4], 2, 8, 2, 4) == 2 * 7 * 2 * 8 * 2 + 2 * 2 * 4 * 8 * 2
+    # prologue: 10 tokens, 8 valid slots, 6 distinct positions, Qwen3 heads, k written out
+    D = 128
+    row = D * 2
+    assert prologue_bytes(10, 8, 6, 16, 8, D, write_k=True) == (
+        10 * 32 * row + 10 * 12 + 6 * D * 4 + 10 * 16 * row + 8 * 16 * row + 10 * 8 * row)

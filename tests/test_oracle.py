@@ -245,12 +245,6 @@ def test_bf16_helpers_round_trip_and_round_to_nearest_even():
     np.testing.assert_array_equal(bits, t)
 
 
-def test_work_counts():
-    assert orc.prefill_flops([2], [2], 1, 1) == 4 * 3
-    assert orc.prefill_flops([1], [5], 2, 4) == 4 * 2 * 4 * 5
-    assert orc.attention_bytes([3, 4], 2, 8, 2, 4) == 2 * 7 * 2 * 8 * 2 + 2 * 2 * 4 * 8 * 2
-
-
 # ---------------------------------------------------------------------------
 # planted mistakes must be caught
 # ---------------------------------------------------------------------------

@@ -178,10 +178,3 @@ def test_qk_norm_rope_store_matches_per_token_loop(cos_sin):
             exp_vc[slots[i]] = row[hq + hkv:]
     assert np.array_equal(kc.reshape(nb * bs, hkv, D), exp_kc)
     assert np.array_equal(vc.reshape(nb * bs, hkv, D), exp_vc)
-
-
-def test_prologue_bytes_counts_each_stream_once():
-    # 10 tokens, 8 valid, 6 distinct positions, Qwen3 heads, k written out
-    b = orc.prologue_bytes(10, 8, 6, 16, 8, D, write_k=True)
-    row = D * 2
-    assert b == 10 * 32 * row + 10 * 12 + 6 * D * 4 + 10 * 16 * row + 8 * 16 * row + 10 * 8 * row
