@@ -5,22 +5,27 @@
 //
 // Mapping (MI355X): the work is a pure HBM copy of 2 * row_bytes per valid
 // token.  One thread owns one VEC-byte chunk at the same offset of the K row
-// and of the V row of kTokensPerThread tokens, so each thread has four
-// independent loads in flight before its four stores; a 256-thread workgroup
-// covers 2 * 256/chunks_per_row whole tokens (4 tokens for a 2 KiB Qwen3-0.6B
-// row).  A token whose slot is -1 costs one 4-byte slot read per thread group.
-// With 16-byte chunks the 4096-token layer step is 1024 workgroups, four per
-// CU from the first wave of dispatch.  Every input row is read once and every
-// cache row written once per step, so loads and stores are non-temporal.
+// and of the V row of U tokens (U = 1, 2, 4 or 8), so each thread has 2U
+// independent loads in flight before its 2U stores; a 256-thread workgroup
+// covers U * 256/chunks_per_row whole tokens.  U is the smallest that keeps
+// the grid within about one round of two workgroups per CU (512 on the 256
+// CUs of an MI355X): the 4096-token layer step runs 512 workgroups of 4
+// tokens per thread.  The rows are loaded whatever their slot, so that no
+// load waits for the slot's (a token whose slot is -1 is read and not
+// written).  Every input row is read once and every cache row written once
+// per step, so loads and stores are non-temporal.
 // Measured on the 4096-token step with inputs and caches cycling through more
-// than the 256 MB Infinity Cache: 9.05 us with cached loads and stores, 7.96
-// us non-temporal (as fast as a plain device copy of the same bytes); 1 token
-// per thread 8.04 us, 4 tokens 9.0 us.
+// than the 256 MB Infinity Cache (interleaved A/B, same process, bit-identical
+// caches): rows loaded after the slot, 1024 workgroups of 2 tokens per thread
+// 8.24 us; rows loaded with the slot: 1024 x 2 tokens 7.40 us, 2048 x 1
+// 7.81 us, 683 x 3 7.56 us, 512 x 4 6.33 us, 342 x 6 7.67 us, 256 x 8 6.57 us.
+// (Earlier, rows after the slot: cached loads and stores 9.05 us against
+// 7.96 us non-temporal.)
 #include "nvk_common.h"
 
 namespace {
 
-constexpr int kTokensPerThread = 2;
+constexpr int kStoreWGs = 640;  // 512 workgroup slots (256 CUs x 2) + 25 %
 
 // Non-temporal 2-, 4- and 16-byte accesses.  Stores go through a by-value
 // copy: indexing the destination with the element of a private array directly
@@ -41,7 +46,7 @@ __device__ __forceinline__ T load_chunk(const T* p) {
     return __builtin_nontemporal_load(p);
 }
 
-template <typename VecT>
+template <typename VecT, int U>
 __global__ __launch_bounds__(256) void kv_store_rows_kernel(
     const char* __restrict__ key, int64_t key_stride_bytes,
     const char* __restrict__ value, int64_t value_stride_bytes,
@@ -49,8 +54,7 @@ __global__ __launch_bounds__(256) void kv_store_rows_kernel(
     const int32_t* __restrict__ slot_mapping, int64_t n_tokens,
     int64_t row_bytes, int chunk_shift, int64_t cache_slots) {
   // chunk_shift = log2(chunks_per_row); a pass covers 256 >> chunk_shift tokens
-  // and a workgroup kTokensPerThread passes.
-  constexpr int U = kTokensPerThread;
+  // and a workgroup U passes.
   const int tid = threadIdx.x;
   const int per_pass = 256 >> chunk_shift;
   const int chunk = tid & ((1 << chunk_shift) - 1);
@@ -61,7 +65,7 @@ __global__ __launch_bounds__(256) void kv_store_rows_kernel(
   for (int u = 0; u < U; ++u) {
     tk[u] = ((int64_t)blockIdx.x * U + u) * per_pass + (tid >> chunk_shift);
     sl[u] = tk[u] < n_tokens ? slot_mapping[tk[u]] : -1;
-    if (sl[u] >= 0 && (int64_t)sl[u] < cache_slots) {
+    if (tk[u] < n_tokens) {  // whatever the slot: the loads do not wait for it
       kx[u] = load_chunk(reinterpret_cast<const VecT*>(key + tk[u] * key_stride_bytes) + chunk);
       vx[u] = load_chunk(reinterpret_cast<const VecT*>(value + tk[u] * value_stride_bytes) + chunk);
     }
@@ -110,11 +114,16 @@ int launch_kv_store(const char* key, int64_t ksb, const char* value, int64_t vsb
   const int64_t cpr = row_bytes / (int64_t)sizeof(VecT);
   const int shift = nvk_log2_exact((int)(cpr <= 256 ? cpr : 0));
   if (shift >= 0) {
-    const int64_t tpb = (256 >> shift) * kTokensPerThread;
-    const int64_t grid = (n_tokens + tpb - 1) / tpb;
-    hipLaunchKernelGGL(kv_store_rows_kernel<VecT>, dim3((unsigned)grid), dim3(256), 0, stream,
-                       key, ksb, value, vsb, kc, vc, slots, n_tokens, row_bytes, shift,
-                       cache_slots);
+    const int64_t per_pass = 256 >> shift;
+    auto grid_of = [&](int u) { return (n_tokens + per_pass * u - 1) / (per_pass * u); };
+    auto launch = [&](auto kernel, int u) {
+      hipLaunchKernelGGL(kernel, dim3((unsigned)grid_of(u)), dim3(256), 0, stream, key, ksb, value,
+                         vsb, kc, vc, slots, n_tokens, row_bytes, shift, cache_slots);
+    };
+    if (grid_of(1) <= kStoreWGs) launch(kv_store_rows_kernel<VecT, 1>, 1);
+    else if (grid_of(2) <= kStoreWGs) launch(kv_store_rows_kernel<VecT, 2>, 2);
+    else if (grid_of(4) <= kStoreWGs) launch(kv_store_rows_kernel<VecT, 4>, 4);
+    else launch(kv_store_rows_kernel<VecT, 8>, 8);
   } else {
     hipLaunchKernelGGL(kv_store_generic_kernel<VecT>, dim3((unsigned)n_tokens), dim3(256), 0,
                        stream, key, ksb, value, vsb, kc, vc, slots, n_tokens, row_bytes,
