@@ -28,10 +28,12 @@ inputs (as many as make one cycle touch >= 1 GiB, 4x the 256 MB Infinity
 Cache, so no step finds its working set cached from the previous use of its
 copy), launches the K-step graph once untimed (its first launch uploads it),
 replays a W-step graph as warmup and keeps replaying it until at least 50 ms
-of warm replays have run (so the clocks are up whatever W is), then brackets
-one more replay of the K-step graph with device synchronisation
-(wall clock -> ms_per_step) and HIP events on the launch stream (-> roofline
-achieved).  Beside the store, a device copy of the same bytes (and one of 512
+of warm replays have run (so the clocks are up whatever W is), then times
+the K-step graph TIMED_REPS times, each replay bracketed by device
+synchronisation (wall clock), alternating with as many replays bracketed by
+HIP events on the launch stream; ms_per_step is the median wall time and
+roofline achieved uses the median event time (a single ~1 ms replay moved
+by 5-10 % with host-side jitter).  Beside the store, a device copy of the same bytes (and one of 512
 MiB) under the same rotation gives the copy rate this box reaches.
 
 CPU baselines run after every GPU leg: the reference's path on the host CPU
@@ -103,7 +105,8 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-MIN_WARM_S = 0.05   # every leg warms for at least this long before its timed replay
+MIN_WARM_S = 0.05   # every leg warms for at least this long before its timed replays
+TIMED_REPS = 5      # timed replays of the K steps; the medians are reported
 
 
 def time_eager(torch, step_fns, steps, warmup):
@@ -117,14 +120,35 @@ def time_eager(torch, step_fns, steps, warmup):
         if i % 8 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
+
+    def run():
+        for i in range(steps):
+            step_fns[i % len(step_fns)]()
+    return timed_reps(torch, run, steps)
+
+
+def timed_reps(torch, run, steps):
+    """TIMED_REPS wall-clock timings of run() (K steps) bracketed by device
+    synchronisation, alternating with TIMED_REPS timings by HIP events on the
+    current stream; returns the medians per step (wall s, event s)."""
+    # The first record of a new event costs ~200 us of host time on MI355X,
+    # which would sit inside the event interval: both are recorded once first.
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
     start.record()
-    for i in range(steps):
-        step_fns[i % len(step_fns)]()
     end.record()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / steps, start.elapsed_time(end) / 1e3 / steps
+    walls, evs = [], []
+    for _ in range(TIMED_REPS):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        run()
+        torch.cuda.synchronize()
+        walls.append((time.perf_counter() - t0) / steps)
+        start.record()
+        run()
+        end.record()
+        torch.cuda.synchronize()
+        evs.append(start.elapsed_time(end) / 1e3 / steps)
+    return statistics.median(walls), statistics.median(evs)
 
 
 def time_graph(torch, step_fns, steps, warmup, eager=False):
@@ -150,13 +174,8 @@ def time_graph(torch, step_fns, steps, warmup, eager=False):
     g_warm = capture(max(1, warmup), 0)
     g = capture(steps, max(1, warmup) % len(step_fns))
     # The first launch of a graph uploads it (measured on MI355X: ~250 us of
-    # host time for a 40-node graph, and ~200 us for the first record of a new
-    # event): both happen here, untimed, so the timed region holds only the
-    # steps themselves.
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
+    # host time for a 40-node graph): it happens here, untimed.
     g.replay()
-    end.record()
     torch.cuda.synchronize()
     t_warm = time.perf_counter()
     g_warm.replay()
@@ -165,14 +184,7 @@ def time_graph(torch, step_fns, steps, warmup, eager=False):
     for _ in range(int((MIN_WARM_S - one) / one) + 1 if one < MIN_WARM_S else 0):
         g_warm.replay()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record()
-    g.replay()
-    end.record()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps
-    ev = start.elapsed_time(end) / 1e3 / steps
-    return wall, ev
+    return timed_reps(torch, g.replay, steps)
 
 
 def cpu_time(fn, reps):
