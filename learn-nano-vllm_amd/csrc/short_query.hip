@@ -8,9 +8,9 @@
 // and LDS work on empty rows here, and one tile per (sequence, kv head) cannot
 // fill the GPU.  This kernel works like the decode kernel instead:
 //   * a wave owns all 16 rows of a (sequence, kv head) group and streams its
-//     keys in chunks of 64; the chunks of all groups are cut into equal
-//     contiguous ranges, one per wave of a persistent grid (stream-K), so
-//     every wave moves the same number of bytes;
+//     keys in chunks of 32; the chunks of all groups are cut into equal
+//     contiguous ranges, one per wave of a persistent grid of one workgroup
+//     per CU (stream-K), so every wave moves the same number of bytes;
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with K loaded straight from the
 //     cache into the A-operand layout: lane (g, r) holds key row r of a 16-key
 //     block, k-step ks covering d = 32ks + 8g .. +7.  The head dimension is
@@ -34,9 +34,17 @@ namespace {
 
 constexpr int HD = 128;
 constexpr int kR = 16;                        // rows per wave (tokens x heads of a kv head)
-constexpr int kCK = 64;                       // keys per chunk
+// Chunks of 32 keys on one workgroup per CU (1024 waves, 16 KiB of K and V
+// in flight per wave).  Measured on MI355X (interleaved A/B, 32 sequences x 6
+// queries over U{1024..8192}; 8 x 6 over U{1024..4096}): 64-key chunks on two
+// workgroups per CU 121.0 / 33.1 us, on one 114.7 / 30.4 us; 32-key chunks on
+// two 119.2 / 33.4 us, on one 113.6 / 29.6 us; 384 workgroups (uneven over
+// the CUs) 134.6 us.  More bytes in flight than this only queue up.
+constexpr int kCK = 32;                       // keys per chunk
+constexpr int kKB = kCK / 16;                 // 16-key blocks of a chunk
+constexpr int kPairs = kCK / 32;              // 32-key pairs (one P.V k-step each)
 constexpr int kWavesPerWG = 4;
-constexpr int kMaxWGs = 512;                  // two workgroups per CU
+constexpr int kMaxWGs = 256;                  // one workgroup per CU
 constexpr int kMinChunks = 2;                 // a wave streams at least this many chunks
 constexpr int kMaxBatch = 2048;
 constexpr int kRowBytes = HD * 2;
@@ -260,9 +268,9 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
   // key 16 kb + r, and its k-step ks covers d = 32 ks + 8 g .. +7 (the head
   // dimension is permuted identically in Q, which leaves q . k unchanged), so
   // the four lanes of a key read 64 contiguous bytes per load.
-  auto issue_k = [&](const ChunkSrc& cs, int rem_rows, vec8 (&kf)[4][HD / 32]) {
+  auto issue_k = [&](const ChunkSrc& cs, int rem_rows, vec8 (&kf)[kKB][HD / 32]) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < kKB; ++kb) {
       const bool ok = 16 * kb + r < rem_rows;
       const uint16_t* src = ok ? cs.k + (int64_t)16 * kb * a.row_elems : a.p.k_cache + 8 * g;
 #pragma unroll
@@ -283,7 +291,7 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
   };
 
   start_group();
-  vec8 kf[4][HD / 32];
+  vec8 kf[kKB][HD / 32];
   {
     const ChunkSrc cs = chunk_src(s, kvh, k, bt_row, nkeys);
     issue_k(cs, rows_of(k, bt_row, nkeys), kf);
@@ -295,9 +303,9 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
     const int kbase = k * kCK;
 
     // ---- S^T = K Q^T (lane: keys 16kb + 4g + i of row r)
-    nvk_f32x4 sacc[4];
+    nvk_f32x4 sacc[kKB];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < kKB; ++kb) {
       sacc[kb] = nvk_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < HD / 32; ++ks)
@@ -331,7 +339,7 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
     const int row_limit = tok + diag;  // last visible key of the row
     float mx = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < kKB; ++kb) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = kbase + 16 * kb + 4 * g + i;
@@ -350,9 +358,9 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
 #pragma unroll
     for (int db = 0; db < HD / 16; ++db) acc_o[db] *= alpha;
     constexpr uint32_t kOnes = E::kOnes;  // the pair (1, 1)
-    vec8 pf[2];
+    vec8 pf[kPairs];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 0; p < kPairs; ++p) {
       uint32_t wds[4];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -370,7 +378,7 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
     }
     // ---- O^T += V^T P^T
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 0; p < kPairs; ++p) {
 #pragma unroll
       for (int db = 0; db < HD / 16; ++db) {
         const uint32_t a_lo = tr_lo + p * 32 * kRowBytes + 32 * (db ^ sw_lo);
