@@ -94,9 +94,9 @@ def test_error_codes_without_launching():
     # a grid of one round of workgroups (3 x 2 query tiles x 8 kv heads): no order
     assert lib.nvk_varlen_prefill_workspace_size(3, 100, 1536, 16, 8, 128) == 0
     # one sequence of 6 queries over 512 keys: no split; the short-query kernels'
-    # records for 64 chunks / 2 per wave = 32 waves
+    # records for 8 kv heads x 16 chunks of 32 keys / 2 per wave = 64 waves
     assert lib.nvk_varlen_prefill_workspace_size(1, 6, 512, 16, 8, 128) == \
-        256 + 32 * 2 * 16 * 132 * 4
+        256 + 64 * 2 * 16 * 132 * 4
     # 9 queries x G 2 = 18 rows: too many for the short path
     assert lib.nvk_varlen_prefill_workspace_size(1, 9, 512, 16, 8, 128) == 0
     # fused prologue: (qkv, stride, T, pos, qw, kw, eps, cos_sin, cs_stride, max_pos, Hq, Hkv,
