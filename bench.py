@@ -320,7 +320,8 @@ def collect_traffic(run_root, out_path):
 def mixed_leg(torch, dev, args, cpu_jobs, layers=28):
     """28 layers of one mixed step, each with its own KV pool (random bf16 made on
     the GPU) and the same block tables / slots; a layer = KV-store of every new
-    token, the prefill chunks, the decodes."""
+    token, then the decodes with the prefill chunks beside them on a second
+    stream, joined before the next layer."""
     from nanovllm_amd import paged_decode, store_kvcache, varlen_prefill
     from nanovllm_amd.flash_api import prefill_tile_order
     from nanovllm_amd.workloads import attention_bytes, mixed_step_metadata, prefill_flops
@@ -345,18 +346,29 @@ def mixed_leg(torch, dev, args, cpu_jobs, layers=28):
     o_pf, o_dec = torch.empty_like(q_pf), torch.empty_like(q_dec)
     scale = 128 ** -0.5
 
+    side = torch.cuda.Stream()   # default priority
+
     def step():
         # the layers share the step's metadata: the prefill tiles are ranked once
         order = prefill_tile_order(t["cu_seqlens_q"], t["cu_seqlens_k"], meta["max_seqlen_q"],
                                    pools[0][0], block_table=t["prefill_block_tables"],
                                    max_seqlen_k=meta["max_seqlen_k"])
+        main = torch.cuda.current_stream()
         for kc, vc in pools:
             store_kvcache(key, value, kc, vc, t["slot_mapping"])
-            varlen_prefill(q_pf, kc, vc, t["cu_seqlens_q"], t["cu_seqlens_k"],
-                           meta["max_seqlen_q"], scale, block_table=t["prefill_block_tables"],
-                           out=o_pf, max_seqlen_k=meta["max_seqlen_k"], order=order)
+            # After the store, the decode takes every workgroup slot first and the
+            # prefill chunks, on a side stream, fill the slots its waves leave as
+            # they finish; the layer ends when both have (321 -> 306 us per layer
+            # on MI355X; the prefill first delays the decode's persistent waves:
+            # 383 us).
+            side.wait_stream(main)
             paged_decode(q_dec, kc, vc, t["context_lens"], t["decode_block_tables"], scale,
                          out=o_dec)
+            with torch.cuda.stream(side):
+                varlen_prefill(q_pf, kc, vc, t["cu_seqlens_q"], t["cu_seqlens_k"],
+                               meta["max_seqlen_q"], scale, block_table=t["prefill_block_tables"],
+                               out=o_pf, max_seqlen_k=meta["max_seqlen_k"], order=order)
+            main.wait_stream(side)
 
     steps, warm = min(args.steps, 10), min(args.warmup, 2)
     log("timing mixed step")
@@ -372,7 +384,8 @@ def mixed_leg(torch, dev, args, cpu_jobs, layers=28):
     return dict(ms_per_step=wall * 1e3, layers=layers, steps=steps,
                 workload="28 layers x (KV-store 4288 tokens + 8 prefill chunks of 512 after "
                          "U{0..1536} cached + 192 decodes over U{256..4096}), 3300-page pool "
-                         "per layer; prefill tiles ranked once per step",
+                         "per layer; prefill tiles ranked once per step; in each layer the "
+                         "decodes run with the prefill chunks beside them on a second stream",
                 per_layer={"decode_bytes": dec_bytes, "prefill_flops": pf_flops,
                            "store_bytes": st_bytes},
                 roofline={"bound": "mixed", "t_roof_ms": round(t_roof * 1e3, 4),
