@@ -70,3 +70,59 @@ def test_tensor_parallel_shard_shapes(hq, hkv):
     assert_attn_close(o, oracle_prefill_paged(pc.q, kc, vc, pc.block_tables, pc.cu_seqlens_q,
                                               pc.cu_seqlens_k, 256, pc.scale),
                       f"shard prefill {hq}/{hkv}")
+
+
+def test_mixed_layer_decode_and_prefill_on_two_streams_match_sequential():
+    """The overlapped order of a mixed step (the decodes on the main stream, the
+    prefill chunks on a second stream after the store, joined afterwards; a
+    graph replays it) gives the sequential order's outputs bit for bit."""
+    case = mixed_layer_case(seed=44, n_chunks=4, chunk=256, cached_hi=800, n_decode=48,
+                            ctx_hi=2000, pool_blocks=420)
+    c = case.to("cuda")
+    say("mixed layer, two streams: store")
+    store_kvcache(c.key, c.value, c.k_cache, c.v_cache, c.slot_mapping)
+
+    def prefill(out):
+        return varlen_prefill(c.q_prefill, c.k_cache, c.v_cache, c.cu_seqlens_q, c.cu_seqlens_k,
+                              case.max_seqlen_q, case.scale, block_table=c.prefill_block_tables,
+                              max_seqlen_k=case.max_seqlen_k, out=out)
+
+    def decode(out):
+        return paged_decode(c.q_decode, c.k_cache, c.v_cache, c.context_lens,
+                            c.decode_block_tables, case.scale, out=out)
+
+    say("mixed layer, two streams: sequential reference")
+    ref_pf, ref_dec = prefill(None), decode(None)
+    torch.cuda.synchronize()
+    o_pf, o_dec = torch.full_like(ref_pf, float("nan")), torch.full_like(ref_dec, float("nan"))
+    side = torch.cuda.Stream()
+
+    def overlapped():
+        main = torch.cuda.current_stream()
+        side.wait_stream(main)
+        decode(o_dec)
+        with torch.cuda.stream(side):
+            prefill(o_pf)
+        main.wait_stream(side)
+
+    say("mixed layer, two streams: eager")
+    overlapped()
+    torch.cuda.synchronize()
+    assert torch.equal(o_pf, ref_pf) and torch.equal(o_dec, ref_dec)
+    say("mixed layer, two streams: graph, three replays")
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        overlapped()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        overlapped()
+    for _ in range(3):
+        o_pf.fill_(float("nan"))
+        o_dec.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o_pf, ref_pf) and torch.equal(o_dec, ref_dec)
