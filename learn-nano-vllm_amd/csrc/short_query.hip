@@ -11,11 +11,18 @@
 //     keys in chunks of 32; the chunks of all groups are cut into equal
 //     contiguous ranges, one per wave of a persistent grid of one workgroup
 //     per CU (stream-K), so every wave moves the same number of bytes;
-//   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with K loaded straight from the
-//     cache into the A-operand layout: lane (g, r) holds key row r of a 16-key
-//     block, k-step ks covering d = 32ks + 8g .. +7.  The head dimension is
-//     permuted the same way in Q, which leaves q . k unchanged and lets the
-//     four lanes of a key read 64 contiguous bytes per load;
+//   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with K in the A-operand
+//     layout: lane (g, r) holds key row r of a 16-key block, k-step ks
+//     covering d = 32ks + 8g .. +7.  The head dimension is permuted the same
+//     way in Q, which leaves q . k unchanged.  When a wave streams many
+//     chunks, K goes through LDS like V (full 256-byte rows per DMA load,
+//     16-byte chunks XOR-swizzled by row & 15, then one ds_read_b128 per
+//     operand); for short ranges it is loaded straight into the operand
+//     layout (the four lanes of a key read 64 contiguous bytes per load), one
+//     LDS round trip less per chunk.  Measured (interleaved A/B): 32 x 6
+//     queries over U{1024..8192} 114.1 -> 109.2 us, 64 x 4 over U{512..4096}
+//     127.2 -> 121.3 us; 8 x 6 over U{1024..4096} 29.4 us in registers
+//     against 31.1 us through LDS;
 //   * the next chunk's K loads go out as soon as the S products have consumed
 //     the registers, its V loads once the P V products have read the LDS
 //     buffer, so a wave always has a chunk in flight;
@@ -46,6 +53,10 @@ constexpr int kPairs = kCK / 32;              // 32-key pairs (one P.V k-step ea
 constexpr int kWavesPerWG = 4;
 constexpr int kMaxWGs = 256;                  // one workgroup per CU
 constexpr int kMinChunks = 2;                 // a wave streams at least this many chunks
+#ifndef NVK_SQ_KLDS_MIN
+#define NVK_SQ_KLDS_MIN 32
+#endif
+constexpr int kKldsMinChunks = NVK_SQ_KLDS_MIN;  // chunks per wave (static bound) for K in LDS
 constexpr int kMaxBatch = 2048;
 constexpr int kRowBytes = HD * 2;
 constexpr int kChunkBytes = kCK * kRowBytes;  // a wave's V staging in LDS
@@ -147,11 +158,13 @@ __device__ __forceinline__ float max_xor16(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-template <bool F16>
+// KLDS: K staged in LDS by full-row DMA loads like V (then read in the MFMA
+// operand layout), instead of loaded straight into the operand layout.
+template <bool F16, bool KLDS>
 __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs a) {
   using E = NvkElt<F16>;
   typedef typename E::vec8 vec8;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kWavesPerWG * kChunkBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[(KLDS ? 2 : 1) * kWavesPerWG * kChunkBytes];
   __shared__ int s_cs[kMaxBatch + 1];
   __shared__ int s_wsum[kWavesPerWG];
   const int tid = threadIdx.x;
@@ -201,12 +214,17 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
   const int sw_lo = rlo & 7, sw_hi = rhi & 7;
   // DMA lane offsets: load j covers rows 4j..4j+3, lane l -> row 4j + l/16,
   // slot l%16, logical chunk (l%16) ^ 2*(row & 7).
-  uint32_t v_voff[kCK / 4];
+  uint32_t v_voff[kCK / 4], k_voff[kCK / 4];
 #pragma unroll
   for (int j = 0; j < kCK / 4; ++j) {
     const int row = 4 * j + g;
     v_voff[j] = (uint32_t)row * a.row_bytes + 16u * (uint32_t)((r) ^ (2 * (row & 7)));
+    k_voff[j] = (uint32_t)row * a.row_bytes + 16u * (uint32_t)(r ^ (row & 15));
   }
+  // KLDS: slot c ^ (row & 15) of a K row holds its logical 16-byte chunk c, so
+  // the operand reads (16 rows, one chunk each, per 16 lanes) are conflict free.
+  const uint32_t kbase_l =
+      KLDS ? (uint32_t)uniform((int)lds_addr(lds + (kWavesPerWG + wave) * kChunkBytes)) : 0u;
 
   // per-group state
   vec8 qf[HD / 32];
@@ -245,6 +263,7 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
   // lane loads and the V buffer descriptor (rows past the keys read zeros).
   struct ChunkSrc {
     const uint16_t* k;  // this lane's K row (a dummy in-bounds row for a missing key)
+    nvk_u32x4 kr;       // KLDS: the K rows' buffer descriptor (SGPRs)
     nvk_u32x4 v;        // SGPRs
   };
   auto chunk_src = [&](int ss, int hh, int kk, const int32_t* btr, int nk) {
@@ -261,6 +280,8 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
     ChunkSrc cs;
     cs.k = (r < rem ? a.p.k_cache + (row0 + r) * a.row_elems + hh * HD : a.p.k_cache) + 8 * g;
     // key blocks 1..3 are rows 16, 32, 48 further; a missing one reads the dummy row
+    if constexpr (KLDS)
+      cs.kr = rsrc_of(a.p.k_cache + row0 * a.row_elems + hh * HD, (uint32_t)rem * a.row_bytes);
     cs.v = rsrc_of(a.p.v_cache + row0 * a.row_elems + hh * HD, (uint32_t)rem * a.row_bytes);
     return cs;
   };
@@ -269,6 +290,11 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
   // dimension is permuted identically in Q, which leaves q . k unchanged), so
   // the four lanes of a key read 64 contiguous bytes per load.
   auto issue_k = [&](const ChunkSrc& cs, int rem_rows, vec8 (&kf)[kKB][HD / 32]) {
+    if constexpr (KLDS) {
+#pragma unroll
+      for (int j = 0; j < kCK / 4; ++j) lds_load(cs.kr, k_voff[j], kbase_l + j * 4 * kRowBytes);
+      return;
+    }
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
       const bool ok = 16 * kb + r < rem_rows;
@@ -308,8 +334,13 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
     for (int kb = 0; kb < kKB; ++kb) {
       sacc[kb] = nvk_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < HD / 32; ++ks)
+      for (int ks = 0; ks < HD / 32; ++ks) {
+        if constexpr (KLDS) {
+          const uint32_t ka = kbase_l + (16 * kb + r) * kRowBytes + 16 * ((4 * ks + g) ^ r);
+          kf[kb][ks] = *reinterpret_cast<const __attribute__((address_space(3))) vec8*>((size_t)ka);
+        }
         sacc[kb] = E::mfma16x16x32(kf[kb][ks], qf[ks], sacc[kb]);
+      }
     }
 
     // ---- the next chunk's position; its K loads go out now (kf is free)
@@ -332,6 +363,8 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
       const int32_t* nbt = a.p.block_tables + (int64_t)ns * a.p.bt_stride;
       const int nkeys_n = ns == s ? nkeys : seq_keys(a, ns);
       nsrc = chunk_src(ns, nkvh, nk, nbt, nkeys_n);
+      // KLDS: this chunk's K reads are done before its buffer is refilled
+      if constexpr (KLDS) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       issue_k(nsrc, rows_of(nk, nbt, nkeys_n), kf);
     }
 
@@ -555,12 +588,19 @@ int short_query_launch(const ShortQueryParams& p, int64_t max_keys, void* ws, hi
   a.desc = static_cast<int32_t*>(ws);
   a.rec = reinterpret_cast<float*>(static_cast<char*>(ws) + sq_desc_bytes(p.batch, p.num_kv_heads));
   a.n_waves = sq_waves(p.batch, max_keys, p.num_kv_heads);
-  if (p.f16)
-    hipLaunchKernelGGL(short_query_kernel<true>, dim3(a.n_waves / kWavesPerWG),
-                       dim3(64 * kWavesPerWG), 0, s, a);
-  else
-    hipLaunchKernelGGL(short_query_kernel<false>, dim3(a.n_waves / kWavesPerWG),
-                       dim3(64 * kWavesPerWG), 0, s, a);
+  // K through LDS when a wave may stream many chunks (its full-row loads
+  // stream faster); straight into registers for short ranges (one LDS round
+  // trip less per chunk).  Bound from the static sizes.
+  const int64_t chunks_bound = (max_keys + kCK - 1) / kCK * p.batch * p.num_kv_heads;
+  const bool klds = chunks_bound >= (int64_t)kKldsMinChunks * a.n_waves;
+  const dim3 grid(a.n_waves / kWavesPerWG), block(64 * kWavesPerWG);
+  if (p.f16) {
+    if (klds) hipLaunchKernelGGL((short_query_kernel<true, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((short_query_kernel<true, false>), grid, block, 0, s, a);
+  } else {
+    if (klds) hipLaunchKernelGGL((short_query_kernel<false, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((short_query_kernel<false, false>), grid, block, 0, s, a);
+  }
   int st = nvk_launch_status();
   if (st != NVK_OK) return st;
   if (p.f16)

@@ -131,6 +131,9 @@ def test_fp16_needles_decode_prefill_short_query():
     run_schedule(NeedleCase(96, lq, [512 + x for x in lq], dtype=F16), pre, 64, "fp16 prefill")
     lk = [int(x) for x in rng.integers(1024, 6000, 12)]
     run_schedule(NeedleCase(97, [6] * 12, lk, dtype=F16), pre, 64, "fp16 short query")
+    # 32 x 6 over contexts up to 8192: the short-query kernel with K staged in LDS
+    lk = [int(x) for x in rng.integers(1024, 8193, 32)]
+    run_schedule(NeedleCase(100, [6] * 32, lk, dtype=F16), pre, 64, "fp16 short query, K in LDS")
 
 
 def test_fp16_noalloc_decode_matches_workspace_decode():
