@@ -30,6 +30,15 @@ def test_store_qwen3_layer_4096_tokens():
     _run_and_check(case, "kv_store 4096 tok, 5% skip")
 
 
+@pytest.mark.parametrize("n_tokens", [1, 1279, 2001, 2560, 5121, 9000])
+def test_store_every_tokens_per_thread_grid(n_tokens):
+    # 2 KiB rows: 1 token per thread up to 1280 tokens, then 2, 4 and 8 (the
+    # grid stays within 640 workgroups), including partial last workgroups
+    pages = (n_tokens + 1000 + 255) // 256
+    case = kv_store_case(seed=12, n_tokens=n_tokens, num_blocks=pages, skip=n_tokens // 20)
+    _run_and_check(case, f"kv_store {n_tokens} tok")
+
+
 def test_store_value_is_packed_qkv_view():
     # v is a view of the packed qkv: row stride (16 + 2*8) * 128 = 4096 elements
     case = kv_store_case(seed=11, n_tokens=777, value_row_stride=4096)
