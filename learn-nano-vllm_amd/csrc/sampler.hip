@@ -23,7 +23,9 @@
 // 64-row step fills the GPU; each workgroup leaves its (score, index) winner
 // in the workspace and a second kernel (one wave per row) picks the row's
 // winner.  The Philox draw (quarter-rate 32x32->64 multiplies) and the two
-// log2 per element, not the logits read, bound the kernel.
+// log2 per element, not the logits read, bound the kernel.  So for large
+// steps (batch x vocab >= 2^24) without the caller's noise, the draw is an
+// inverse-CDF one instead (two uniforms per row; see sample_mass_kernel).
 #include "nvk_common.h"
 
 namespace {
@@ -70,6 +72,7 @@ struct SampleArgs {
   int64_t* tokens;
 };
 
+constexpr int64_t kCdfMinElements = int64_t{1} << 24;  // batch x vocab for the inverse-CDF path
 constexpr int kPartThreads = 256;
 constexpr int kIters = 4;
 constexpr int kChunk = kPartThreads * 8 * kIters;  // elements of a row per workgroup
@@ -209,6 +212,202 @@ __global__ __launch_bounds__(256) void sample_final_kernel(SampleArgs a, int bat
   if (lane == 0) a.tokens[row] = best_i == 0x7fffffff ? 0 : best_i;
 }
 
+// ---- the kernel's own randomness: inverse-CDF sampling ----------------------
+// Without the caller's noise the token is drawn by inverse transform over the
+// row's softmax, with two uniforms per row instead of one exponential per
+// element (the Philox draw per element, not the logits read, bounded the
+// race): the mass kernel reduces every chunk of the row to its maximum M_c of
+// x_i = logits_i * log2(e) / T and S_c = sum_i 2^(x_i - M_c); the pick kernel
+// draws (u1, u2) from Philox4x32-10 keyed by (seed) at counter (offset, row),
+// selects chunk c with probability S_c 2^(M_c - M) / sum, then the first index
+// of that chunk whose running sum of 2^(x_i - M_c) reaches u2 S_c.  A token is
+// drawn with probability p_i up to float32 rounding of the running sums (a
+// token with less than ~2^-24 of its chunk's mass is not drawn).  Rows with no
+// finite score give token 0, as in the race.
+
+// x of one element (non-finite logits: -inf, no mass)
+__device__ __forceinline__ float mass_x(float l, float scale) {
+  const float x = l * scale;
+  return (x == x && x != INFINITY) ? x : -INFINITY;
+}
+
+__device__ __forceinline__ float block_max256(float v, float* red) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+// Exclusive prefix of v over the 256 threads (in thread order); *total = sum.
+__device__ __forceinline__ float block_excl256(float v, float* red, float* total) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  float x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  __syncthreads();
+  if (lane == 63) red[w] = x;
+  __syncthreads();
+  float before = 0.f;
+  for (int i = 0; i < w; ++i) before += red[i];
+  *total = (red[0] + red[1]) + (red[2] + red[3]);
+  return before + x - v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kPartThreads) void sample_mass_kernel(SampleArgs a) {
+  static_assert(kPartThreads == 256, "block reductions assume 256 threads");
+  const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+  __shared__ float red[4];
+  const float scale = NVK_LOG2E / a.temperatures[row];
+  float x[kIters][8];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int it = 0; it < kIters; ++it) {
+    const int base = c * kChunk + (it * kPartThreads + tid) * 8;
+    float l[8];
+    if (base < a.vocab) {
+      load8<T>(a, row, base, base + 8 <= a.vocab, l);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) l[i] = -INFINITY;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[it][i] = mass_x(l[i], scale);
+      mx = fmaxf(mx, x[it][i]);
+    }
+  }
+  const float M = block_max256(mx, red);
+  float sum = 0.f;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int it = 0; it < kIters; ++it)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sum += exp2f(x[it][i] - M);
+  }
+  const float S = block_sum256(sum, red);
+  if (tid == 0) {
+    a.part_score[(int64_t)row * a.chunks + c] = M;
+    reinterpret_cast<float*>(a.part_index)[(int64_t)row * a.chunks + c] = S;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void sample_pick_kernel(SampleArgs a) {
+  const int row = blockIdx.x, tid = threadIdx.x;
+  __shared__ float red[4];
+  const float* pm = a.part_score + (int64_t)row * a.chunks;
+  const float* ps = reinterpret_cast<const float*>(a.part_index) + (int64_t)row * a.chunks;
+  float m = -INFINITY;
+  for (int c = tid; c < a.chunks; c += 256) m = fmaxf(m, pm[c]);
+  const float Mg = block_max256(m, red);
+  if (Mg == -INFINITY) {  // no finite score in the row
+    if (tid == 0) a.tokens[row] = 0;
+    return;
+  }
+  auto weight = [&](int c) { return c < a.chunks && pm[c] != -INFINITY ? ps[c] * exp2f(pm[c] - Mg) : 0.f; };
+  float wsum = 0.f;
+  for (int c = tid; c < a.chunks; c += 256) wsum += weight(c);
+  const float W = block_sum256(wsum, red);
+  // two uniforms in (0, 1] for this row and call
+  const U4 r = philox10(U4{(uint32_t)a.offset, (uint32_t)(a.offset >> 32), (uint32_t)row, 1u},
+                        (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
+  const float u1 = ((float)r.x + 1.0f) * 2.3283064365386963e-10f;
+  const float u2 = ((float)r.y + 1.0f) * 2.3283064365386963e-10f;
+  // chunk: the first whose running weight reaches u1 W (rounding: the last with weight)
+  const float t1 = u1 * W;
+  float run = 0.f;
+  int pick = a.chunks, last_pos = -1;
+  for (int base = 0; base < a.chunks; base += 256) {
+    const int c = base + tid;
+    const float wc = weight(c);
+    float tot;
+    const float ex = block_excl256(wc, red, &tot);
+    const int hit = (wc > 0.f && run + ex + wc >= t1) ? c : a.chunks;
+    const int lp = wc > 0.f ? c : -1;
+    // smallest hit and largest positive chunk over the block
+    int h = hit, l = lp;
+#pragma unroll
+    for (int mm = 32; mm >= 1; mm >>= 1) {
+      h = min(h, __shfl_xor(h, mm));
+      l = max(l, __shfl_xor(l, mm));
+    }
+    __shared__ int s_h[4], s_l[4];
+    __syncthreads();
+    if ((tid & 63) == 0) { s_h[tid >> 6] = h; s_l[tid >> 6] = l; }
+    __syncthreads();
+    pick = min(pick, min(min(s_h[0], s_h[1]), min(s_h[2], s_h[3])));
+    last_pos = max(last_pos, max(max(s_l[0], s_l[1]), max(s_l[2], s_l[3])));
+    run += tot;
+  }
+  if (pick >= a.chunks) pick = last_pos;
+  // element: the first of the chunk whose running mass reaches u2 S_c
+  const float Mc = pm[pick];
+  const float t2 = u2 * ps[pick];
+  const float scale = NVK_LOG2E / a.temperatures[row];
+  float e[32];  // the thread's 32 elements, in index order
+  float tsum = 0.f;
+  const int first = pick * kChunk + 32 * tid;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int base = first + 8 * j;
+    float l[8];
+    if (base < a.vocab) {
+      load8<T>(a, row, base, base + 8 <= a.vocab, l);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) l[i] = -INFINITY;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      e[8 * j + i] = exp2f(mass_x(l[i], scale) - Mc);
+      tsum += e[8 * j + i];
+    }
+  }
+  float tot;
+  const float ex = block_excl256(tsum, red, &tot);
+  int found = a.vocab, lastpos = -1;
+  for (int i = 31; i >= 0; --i)
+    if (e[i] > 0.f) { lastpos = first + i; break; }
+  if (tsum > 0.f && ex < t2 && t2 <= ex + tsum) {  // the target falls in this thread's run
+    float cum = ex;
+    found = lastpos;  // if rounding keeps the running sum below the target
+    for (int i = 0; i < 32; ++i) {
+      cum += e[i];
+      if (e[i] > 0.f && cum >= t2) { found = first + i; break; }
+    }
+  }
+  int fnd = found, lst = lastpos;
+#pragma unroll
+  for (int mm = 32; mm >= 1; mm >>= 1) {
+    fnd = min(fnd, __shfl_xor(fnd, mm));
+    lst = max(lst, __shfl_xor(lst, mm));
+  }
+  __shared__ int s_f[4], s_ls[4];
+  __syncthreads();
+  if ((tid & 63) == 0) { s_f[tid >> 6] = fnd; s_ls[tid >> 6] = lst; }
+  __syncthreads();
+  if (tid == 0) {
+    int tok = min(min(s_f[0], s_f[1]), min(s_f[2], s_f[3]));
+    if (tok >= a.vocab) tok = max(max(s_ls[0], s_ls[1]), max(s_ls[2], s_ls[3]));
+    a.tokens[row] = tok < 0 ? 0 : tok;
+  }
+}
+
 struct GatherArgs {
   const uint16_t* x;
   int64_t x_row_stride;
@@ -267,6 +466,20 @@ extern "C" int nvk_sample(const void* logits, int64_t row_stride, int32_t batch,
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(a.chunks, batch);
   const bool bf16 = dtype == NVK_DTYPE_BF16;
+  // The kernel's own randomness: the exponential race for small steps (one
+  // pass, its Philox draws per element cheap enough), inverse-CDF over the
+  // chunk masses for large ones (two draws per row; its pick kernel adds a
+  // fixed ~8 us).  Measured on MI355X, vocab 151936: B = 64 race 14.8 us,
+  // inverse-CDF 16.8 us; B = 512 race 58.5 us, inverse-CDF 45.4 us.
+  if (!noise && (int64_t)batch * vocab >= kCdfMinElements) {
+    if (bf16) hipLaunchKernelGGL((sample_mass_kernel<uint16_t>), grid, dim3(kPartThreads), 0, s, a);
+    else hipLaunchKernelGGL((sample_mass_kernel<float>), grid, dim3(kPartThreads), 0, s, a);
+    int st = nvk_launch_status();
+    if (st != NVK_OK) return st;
+    if (bf16) hipLaunchKernelGGL((sample_pick_kernel<uint16_t>), dim3(batch), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((sample_pick_kernel<float>), dim3(batch), dim3(256), 0, s, a);
+    return nvk_launch_status();
+  }
   if (bf16 && noise)
     hipLaunchKernelGGL((sample_partial_kernel<uint16_t, true>), grid, dim3(kPartThreads), 0, s, a);
   else if (bf16)

@@ -103,6 +103,47 @@ def test_philox_draws_follow_softmax(temp):
     assert stats.chisquare(counts, p * counts.sum()).pvalue > 1e-4
 
 
+def test_draws_across_vocab_chunks_follow_softmax():
+    # mass spread over five 8192-token chunks of the row (chunk edges included):
+    # the chunk is drawn by its mass, then the token inside it
+    say("sampler draws across chunks")
+    v, rows, calls = 40000, 4096, 10
+    hot = [5, 8191, 8192, 12000, 16383, 20000, 24576, 30000, 35000, 39999]
+    vals = torch.linspace(-1.0, 1.2, len(hot))
+    base = torch.full((v,), -40.0)
+    base[hot] = vals
+    logits = base.to(torch.bfloat16).repeat(rows, 1).cuda()
+    temps = torch.ones(rows, device="cuda")
+    toks = torch.cat([_raw_sample(logits, temps, 5, k * 10007) for k in range(calls)]).cpu().numpy()
+    assert np.isin(toks, hot).all()
+    counts = np.array([(toks == h).sum() for h in hot])
+    x = base.to(torch.bfloat16).float().numpy()[hot].astype(np.float64)
+    p = np.exp(x - x.max())
+    p /= p.sum()
+    assert stats.chisquare(counts, p * counts.sum()).pvalue > 1e-4
+
+
+def test_draws_uniform_over_a_partial_last_chunk():
+    say("sampler partial last chunk")
+    v = 8197                                                  # 8192 + 5
+    logits = torch.zeros(2048, v, dtype=torch.float32, device="cuda")
+    temps = torch.ones(2048, device="cuda")
+    toks = torch.cat([_raw_sample(logits, temps, 9, k * 4099) for k in range(20)]).cpu().numpy()
+    assert toks.min() >= 0 and toks.max() < v
+    counts = np.bincount(toks * 11 // v, minlength=11)       # 11 equal bins
+    expected = np.bincount(np.arange(v) * 11 // v, minlength=11) / v * toks.size
+    assert stats.chisquare(counts, expected).pvalue > 1e-4
+    # the last chunk's five tokens are drawn at their share
+    assert abs((toks >= 8192).mean() - 5 / v) < 5 * np.sqrt(5 / v / toks.size)
+
+
+def test_rows_without_finite_logits_give_token_zero():
+    logits = torch.full((3, 100), float("-inf"), device="cuda")
+    logits[1, 37] = 0.0
+    out = _raw_sample(logits, torch.ones(3, device="cuda"), 1, 0).cpu().tolist()
+    assert out == [0, 37, 0]
+
+
 def test_last_token_gather_and_lm_head():
     say("lm head gather")
     g = torch.Generator().manual_seed(3)
