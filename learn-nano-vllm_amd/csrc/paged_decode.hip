@@ -40,7 +40,9 @@
 // partial (o, m, l) record per wave and head; every wave also writes the
 // group's descriptor (its first and last wave), so a small combine kernel
 // merges the cut groups after two dependent reads and writes the zero rows of
-// empty contexts.  (Merging inside the main kernel needs cross-XCD release /
+// empty contexts.  Steps with few groups and long contexts (a group cut into
+// up to 256 parts) use a combine whose 16 waves fold interleaved slices of the
+// parts and merge them through LDS.  (Merging inside the main kernel needs cross-XCD release /
 // acquire fences per part; on MI355X those cost far more than the combine.)
 #include <mutex>
 
@@ -57,6 +59,10 @@ constexpr int kMaxBatch = 2048;    // sequences per call (LDS prefix table)
 // takes a 4-sequence decode from 30 to 17 us and a 16-sequence one from 34 to
 // 27 us (more waves share a small step), and changes nothing from 64 up.
 constexpr int kMinChunks = 2;
+#ifndef NVK_DECODE_SLICE_MIN_WAVES
+#define NVK_DECODE_SLICE_MIN_WAVES 32
+#endif
+constexpr int kSliceMinWaves = NVK_DECODE_SLICE_MIN_WAVES;
 
 typedef __attribute__((address_space(4))) const int32_t nvk_const_i32;
 typedef __attribute__((address_space(4))) const int64_t nvk_const_i64;
@@ -563,23 +569,23 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 }
 
 // Merges the partial records of groups cut between waves and writes the zero
-// output of empty contexts.  grid = (Hkv, B), block = G*HD threads.
+// output of empty contexts.
 // Merge of one output element over the parts of a cut group: wave p1's head
 // record (slot 0) and the continuation records (slot 1) of waves p1+1 .. p2
 // (every active wave's range holds at least kMinChunks chunks, so each of
-// them wrote one).  kBatch parts are fetched per round trip (3 kBatch loads
-// in flight), then folded into (M, L, O).  rec0: the record of wave 0, slot
-// 0, for this thread's kv head and q head.
+// them wrote one).  A slice s of S folds parts p1+s, p1+s+S, ...; kBatch
+// parts are fetched per round trip (3 kBatch loads in flight), then folded
+// into (M, L, O).  rec0: the record of wave 0, slot 0, for this thread's kv
+// head and q head.
 template <int kBatch, int HD, int G>
-__device__ __forceinline__ float merge_parts(const DecodeArgs& a, const float* rec0, int p1,
-                                             int p2, int d) {
+__device__ __forceinline__ void fold_parts(const DecodeArgs& a, const float* rec0, int p1, int p2,
+                                           int s, int S, int d, float& M, float& L, float& O) {
   constexpr int REC_HEAD = G * (HD + 4);
-  float M = -INFINITY, L = 0.f, O = 0.f;
-  for (int base = p1; base <= p2; base += kBatch) {
+  for (int base = p1 + s; base <= p2; base += kBatch * S) {
     float mv[kBatch], lv[kBatch], ov[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int p = base + u;
+      const int p = base + u * S;
       const bool ok = p <= p2;
       const int pr = ok ? p : p1;
       const float* rec = rec0 + ((int64_t)pr * 2 + (pr == p1 ? 0 : 1)) * a.hpi * REC_HEAD;
@@ -607,9 +613,10 @@ __device__ __forceinline__ float merge_parts(const DecodeArgs& a, const float* r
     }
     M = mb;
   }
-  return L > 0.f ? O / L : 0.f;
 }
 
+// grid = (Hkv, B), block = G*HD threads, one per output element of the
+// (sequence, kv head).
 template <int HD, int G, bool F16>
 __global__ __launch_bounds__(G * HD) void paged_decode_combine_kernel(DecodeArgs a) {
   constexpr int REC_HEAD = G * (HD + 4);  // floats per kv head in a record
@@ -626,11 +633,71 @@ __global__ __launch_bounds__(G * HD) void paged_decode_combine_kernel(DecodeArgs
   const int p1 = desc.x, p2 = desc.y;
   if (p1 == p2) return;  // finished inside one wave
   const float* rec0 = a.ws_rec + hh * REC_HEAD + h * (HD + 4);
+  float M = -INFINITY, L = 0.f, O = 0.f;
   // groups cut into many parts (small batches, long contexts) fetch 32 per
   // round trip; the others 16 (uniform over the workgroup)
-  const float r = p2 - p1 < 16 ? merge_parts<16, HD, G>(a, rec0, p1, p2, d)
-                               : merge_parts<32, HD, G>(a, rec0, p1, p2, d);
-  *op = NvkElt<F16>::one(r);
+  if (p2 - p1 < 16)
+    fold_parts<16, HD, G>(a, rec0, p1, p2, 0, 1, d, M, L, O);
+  else
+    fold_parts<32, HD, G>(a, rec0, p1, p2, 0, 1, d, M, L, O);
+  *op = NvkElt<F16>::one(L > 0.f ? O / L : 0.f);
+}
+
+// Combine of steps whose groups are cut into many parts (few sequences, long
+// contexts: a 1-sequence step over 16 K keys cuts each group into 256).
+// grid = (Hkv * G*HD/64, B), block = kSlices waves; a workgroup owns 64
+// consecutive output elements of one (sequence, kv head), wave s folds parts
+// p1+s, p1+s+kSlices, ... (so a thread waits for 1/kSlices of the round
+// trips), and wave 0 merges the waves' (M, L, O) through LDS.
+constexpr int kSlices = 16;
+template <int HD, int G, bool F16>
+__global__ __launch_bounds__(64 * kSlices) void paged_decode_combine_sliced_kernel(DecodeArgs a) {
+  constexpr int REC_HEAD = G * (HD + 4);
+  constexpr int EB = G * HD / 64;  // workgroups per (sequence, kv head)
+  const int kvh = blockIdx.x / EB, b = blockIdx.y;
+  const int lane = threadIdx.x & 63, s = threadIdx.x >> 6;
+  const int e = (blockIdx.x % EB) * 64 + lane;
+  const int h = e / HD, d = e % HD;
+  const int n_blk = a.num_kv_heads / a.hpi;
+  const int hh = kvh % a.hpi;
+  const int2 desc = *reinterpret_cast<const int2*>(a.ws_desc + 2 * (b * n_blk + kvh / a.hpi));
+  uint16_t* op = a.out + (int64_t)b * a.out_stride_tok + (int64_t)(kvh * G + h) * a.out_stride_head + d;
+  if (desc.x < 0) {  // empty context (padded graph row): defined zero output
+    if (s == 0) *op = 0;
+    return;
+  }
+  const int p1 = desc.x, p2 = desc.y;
+  if (p1 == p2) return;  // finished inside one wave (uniform over the workgroup)
+  const float* rec0 = a.ws_rec + hh * REC_HEAD + h * (HD + 4);
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  const int per_slice = (p2 - p1 + kSlices) / kSlices;  // ceil(parts / kSlices)
+  if (per_slice <= 4)
+    fold_parts<4, HD, G>(a, rec0, p1, p2, s, kSlices, d, M, L, O);
+  else if (per_slice <= 8)
+    fold_parts<8, HD, G>(a, rec0, p1, p2, s, kSlices, d, M, L, O);
+  else if (per_slice <= 16)
+    fold_parts<16, HD, G>(a, rec0, p1, p2, s, kSlices, d, M, L, O);
+  else
+    fold_parts<32, HD, G>(a, rec0, p1, p2, s, kSlices, d, M, L, O);
+  __shared__ float sm[kSlices][64], sl[kSlices][64], so[kSlices][64];
+  sm[s][lane] = M;
+  sl[s][lane] = L;
+  so[s][lane] = O;
+  __syncthreads();
+  if (s != 0) return;
+  float mx = sm[0][lane];
+#pragma unroll
+  for (int i = 1; i < kSlices; ++i) mx = fmaxf(mx, sm[i][lane]);
+  const float mref = mx == -INFINITY ? 0.f : mx;
+  L = 0.f;
+  O = 0.f;
+#pragma unroll
+  for (int i = 0; i < kSlices; ++i) {
+    const float wt = nvk_fast_exp2(sm[i][lane] - mref);
+    L += sl[i][lane] * wt;
+    O += so[i][lane] * wt;
+  }
+  *op = NvkElt<F16>::one(L > 0.f ? O / L : 0.f);
 }
 
 // kv heads per load instruction.  One: a group is then one (sequence, kv
@@ -680,8 +747,16 @@ int launch_decode(const DecodeArgs& a, bool aligned, hipStream_t stream) {
                        stream, a);
   int st = nvk_launch_status();
   if (st != NVK_OK) return st;
-  hipLaunchKernelGGL((paged_decode_combine_kernel<HD, G, F16>), dim3(a.num_kv_heads, a.batch),
-                     dim3(G * HD), 0, stream, a);
+  // Steps with at least NVK_DECODE_SLICE_MIN_WAVES waves per group cut
+  // their groups into many parts: the sliced combine folds them.
+  const int64_t groups = (int64_t)a.batch * (a.num_kv_heads / a.hpi);
+  if (a.n_waves >= (int64_t)kSliceMinWaves * groups)
+    hipLaunchKernelGGL((paged_decode_combine_sliced_kernel<HD, G, F16>),
+                       dim3(a.num_kv_heads * (G * HD / 64), a.batch), dim3(64 * kSlices), 0,
+                       stream, a);
+  else
+    hipLaunchKernelGGL((paged_decode_combine_kernel<HD, G, F16>), dim3(a.num_kv_heads, a.batch),
+                       dim3(G * HD), 0, stream, a);
   return nvk_launch_status();
 }
 
