@@ -33,7 +33,9 @@
 //     ds_read_b64_tr_b16 per operand (16-byte chunks of each 256-byte row
 //     XOR-swizzled by 2*(row & 7): conflict-free);
 //   * online softmax per chunk in log2 units; groups cut between waves leave
-//     (O, m, l) records that a combine kernel merges, as in the decode.
+//     (O, m, l) records that a combine kernel merges, as in the decode (with
+//     16 waves folding interleaved slices of the parts when groups are cut
+//     into many).
 #include "nvk_common.h"
 #include "short_query.h"
 
@@ -473,23 +475,23 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
 }
 
 // Merges the records of groups cut between waves and writes the zero rows of
-// groups with no key.  grid = (Hkv, batch), 512 threads: thread t owns row
-// t / 32 and d = 4 (t % 32) .. +3.
-// Merge of one row's 4 output columns over the parts p1..p2 of a cut group
-// (wave p1's head record, slot 0, then the continuation records, slot 1),
-// kBatch parts per round trip; returns the unnormalised sum O and its L.
+// groups with no key.
+// Merge of one row's 4 output columns over the parts of a cut group (wave
+// p1's head record, slot 0, then the continuation records, slot 1): slice s
+// of S folds parts p1+s, p1+s+S, ..., kBatch parts per round trip; returns
+// the unnormalised sum O, its L and the reference max M.
 template <int kBatch>
 __device__ __forceinline__ void sq_merge_parts(const SqArgs& a, int row, int d0, int p1, int p2,
-                                               float& L, nvk_f32x4& O) {
-  float M = -INFINITY;
+                                               int s, int S, float& M, float& L, nvk_f32x4& O) {
+  M = -INFINITY;
   L = 0.f;
   O = nvk_f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int base = p1; base <= p2; base += kBatch) {
+  for (int base = p1 + s; base <= p2; base += kBatch * S) {
     float mv[kBatch], lv[kBatch];
     nvk_f32x4 ov[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int p = base + u;
+      const int p = base + u * S;
       const bool ok = p <= p2;
       const int pr = ok ? p : p1;
       const float* rec = a.rec + (((int64_t)pr * 2 + (pr == p1 ? 0 : 1)) * kR + row) * kRec;
@@ -515,6 +517,17 @@ __device__ __forceinline__ void sq_merge_parts(const SqArgs& a, int row, int d0,
 }
 
 template <bool F16>
+__device__ __forceinline__ void sq_write_row(uint16_t* op, float L, const nvk_f32x4& O) {
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  nvk_u32x2 wv;
+  wv.x = NvkElt<F16>::pack2(O[0] * inv, O[1] * inv);
+  wv.y = NvkElt<F16>::pack2(O[2] * inv, O[3] * inv);
+  *reinterpret_cast<nvk_u32x2*>(op) = wv;
+}
+
+// grid = (Hkv, batch), 512 threads: thread t owns row t / 32 and
+// d = 4 (t % 32) .. +3.
+template <bool F16>
 __global__ __launch_bounds__(512) void short_query_combine_kernel(SqArgs a) {
   const int kvh = blockIdx.x, s = blockIdx.y;
   const int row = threadIdx.x >> 5, d0 = 4 * (threadIdx.x & 31);
@@ -533,17 +546,70 @@ __global__ __launch_bounds__(512) void short_query_combine_kernel(SqArgs a) {
   if (p1 == p2) return;  // finished inside one wave
   // groups cut into more than 8 parts fetch 16 per round trip (uniform over
   // the workgroup)
-  float L;
+  float M, L;
   nvk_f32x4 O;
   if (p2 - p1 < 8)
-    sq_merge_parts<8>(a, row, d0, p1, p2, L, O);
+    sq_merge_parts<8>(a, row, d0, p1, p2, 0, 1, M, L, O);
   else
-    sq_merge_parts<16>(a, row, d0, p1, p2, L, O);
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  nvk_u32x2 wv;
-  wv.x = NvkElt<F16>::pack2(O[0] * inv, O[1] * inv);
-  wv.y = NvkElt<F16>::pack2(O[2] * inv, O[3] * inv);
-  *reinterpret_cast<nvk_u32x2*>(op) = wv;
+    sq_merge_parts<16>(a, row, d0, p1, p2, 0, 1, M, L, O);
+  sq_write_row<F16>(op, L, O);
+}
+
+// Combine of steps whose groups are cut into many parts (one to four
+// sequences over long contexts: 1 x 16 K keys cuts each group into 128).
+// grid = (Hkv * kR/2, batch), kSqSlices waves: a workgroup owns two rows of
+// one (sequence, kv head), wave s folds parts p1+s, p1+s+kSqSlices, ... (half
+// a wave per row, 4 columns per lane), and wave 0 merges the waves' states
+// through LDS.
+constexpr int kSqSlices = 16;
+template <bool F16>
+__global__ __launch_bounds__(64 * kSqSlices) void short_query_combine_sliced_kernel(SqArgs a) {
+  const int kvh = blockIdx.x / (kR / 2), s = blockIdx.y;
+  const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
+  const int row = 2 * (blockIdx.x % (kR / 2)) + (lane >> 5), d0 = 4 * (lane & 31);
+  const int Lq = seq_queries(a, s);
+  if (2 * (blockIdx.x % (kR / 2)) >= Lq * a.G) return;  // both rows empty (uniform)
+  const bool row_ok = row < Lq * a.G;
+  const int tok = row / a.G;
+  const int head = kvh * a.G + row % a.G;
+  uint16_t* op = a.p.out + (int64_t)(a.p.cu_q[s] + tok) * a.p.out_stride_tok +
+                 (int64_t)head * a.p.out_stride_head + d0;
+  const int2 desc = *reinterpret_cast<const int2*>(a.desc + 2 * (s * a.p.num_kv_heads + kvh));
+  if (desc.x < 0) {  // uniform over the workgroup
+    if (slice == 0 && row_ok) *reinterpret_cast<nvk_u32x2*>(op) = nvk_u32x2{0u, 0u};
+    return;
+  }
+  const int p1 = desc.x, p2 = desc.y;
+  if (p1 == p2) return;  // finished inside one wave (uniform)
+  float M, L;
+  nvk_f32x4 O;
+  const int per_slice = (p2 - p1 + kSqSlices) / kSqSlices;  // ceil(parts / kSqSlices)
+  if (per_slice <= 4)
+    sq_merge_parts<4>(a, row, d0, p1, p2, slice, kSqSlices, M, L, O);
+  else if (per_slice <= 8)
+    sq_merge_parts<8>(a, row, d0, p1, p2, slice, kSqSlices, M, L, O);
+  else
+    sq_merge_parts<16>(a, row, d0, p1, p2, slice, kSqSlices, M, L, O);
+  __shared__ float sm[kSqSlices][64], sl[kSqSlices][64];
+  __shared__ nvk_f32x4 so[kSqSlices][64];
+  sm[slice][lane] = M;
+  sl[slice][lane] = L;
+  so[slice][lane] = O;
+  __syncthreads();
+  if (slice != 0 || !row_ok) return;
+  float mx = sm[0][lane];
+#pragma unroll
+  for (int i = 1; i < kSqSlices; ++i) mx = fmaxf(mx, sm[i][lane]);
+  const float mref = mx == -INFINITY ? 0.f : mx;
+  L = 0.f;
+  O = nvk_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kSqSlices; ++i) {
+    const float wt = nvk_fast_exp2(sm[i][lane] - mref);
+    L += sl[i][lane] * wt;
+    O += wt * so[i][lane];
+  }
+  sq_write_row<F16>(op, L, O);
 }
 
 int sq_waves(int batch, int64_t max_keys, int num_kv_heads) {
@@ -603,11 +669,19 @@ int short_query_launch(const ShortQueryParams& p, int64_t max_keys, void* ws, hi
   }
   int st = nvk_launch_status();
   if (st != NVK_OK) return st;
-  if (p.f16)
-    hipLaunchKernelGGL(short_query_combine_kernel<true>, dim3(p.num_kv_heads, p.batch),
-                       dim3(32 * kR), 0, s, a);
+  // At least 32 waves per (sequence, kv head) group: its parts are folded in
+  // slices.
+  const bool sliced = a.n_waves >= 32 * (int64_t)p.batch * p.num_kv_heads;
+  const dim3 sgrid(p.num_kv_heads * (kR / 2), p.batch), cgrid(p.num_kv_heads, p.batch);
+  if (sliced && p.f16)
+    hipLaunchKernelGGL(short_query_combine_sliced_kernel<true>, sgrid, dim3(64 * kSqSlices), 0, s,
+                       a);
+  else if (sliced)
+    hipLaunchKernelGGL(short_query_combine_sliced_kernel<false>, sgrid, dim3(64 * kSqSlices), 0,
+                       s, a);
+  else if (p.f16)
+    hipLaunchKernelGGL(short_query_combine_kernel<true>, cgrid, dim3(32 * kR), 0, s, a);
   else
-    hipLaunchKernelGGL(short_query_combine_kernel<false>, dim3(p.num_kv_heads, p.batch),
-                       dim3(32 * kR), 0, s, a);
+    hipLaunchKernelGGL(short_query_combine_kernel<false>, cgrid, dim3(32 * kR), 0, s, a);
   return nvk_launch_status();
 }

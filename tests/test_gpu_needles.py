@@ -89,6 +89,10 @@ def test_dense_prefill_needles(lens, hq, hkv):
     ("2 queries, G=8", 2, _lens(15, 12, 64, 5000), 16, 2),
     ("16 queries, G=1", 16, _lens(16, 6, 64, 3000), 16, 16),
     ("batch 4, long contexts cut into many parts", 6, [8192, 7000, 6100, 4321], 16, 8),
+    # the sliced combine: one sequence's groups cut into ~128 parts; three
+    # query rows of G=1, so a workgroup's second row is past the last one
+    ("1 sequence over 16384 keys", 6, [16384], 16, 8),
+    ("3 queries over 2 long sequences, G=1", 3, [9000, 12000], 16, 16),
 ])
 def test_short_query_needles(name, nq, lens, hq, hkv):
     case = NeedleCase(13, [nq] * len(lens), lens, block_size=256, hq=hq, hkv=hkv)
