@@ -634,9 +634,14 @@ __global__ __launch_bounds__(G * HD) void paged_decode_combine_kernel(DecodeArgs
   if (p1 == p2) return;  // finished inside one wave
   const float* rec0 = a.ws_rec + hh * REC_HEAD + h * (HD + 4);
   float M = -INFINITY, L = 0.f, O = 0.f;
-  // groups cut into many parts (small batches, long contexts) fetch 32 per
-  // round trip; the others 16 (uniform over the workgroup)
-  if (p2 - p1 < 16)
+  // records fetched per round trip: the smallest batch that holds every part
+  // (32 for groups cut into more; uniform over the workgroup)
+  const int parts = p2 - p1 + 1;
+  if (parts <= 4)
+    fold_parts<4, HD, G>(a, rec0, p1, p2, 0, 1, d, M, L, O);
+  else if (parts <= 8)
+    fold_parts<8, HD, G>(a, rec0, p1, p2, 0, 1, d, M, L, O);
+  else if (parts <= 16)
     fold_parts<16, HD, G>(a, rec0, p1, p2, 0, 1, d, M, L, O);
   else
     fold_parts<32, HD, G>(a, rec0, p1, p2, 0, 1, d, M, L, O);
