@@ -544,11 +544,14 @@ __global__ __launch_bounds__(512) void short_query_combine_kernel(SqArgs a) {
   }
   const int p1 = desc.x, p2 = desc.y;
   if (p1 == p2) return;  // finished inside one wave
-  // groups cut into more than 8 parts fetch 16 per round trip (uniform over
-  // the workgroup)
+  // records fetched per round trip: the smallest batch that holds every part
+  // (16 for groups cut into more; uniform over the workgroup)
   float M, L;
   nvk_f32x4 O;
-  if (p2 - p1 < 8)
+  const int parts = p2 - p1 + 1;
+  if (parts <= 4)
+    sq_merge_parts<4>(a, row, d0, p1, p2, 0, 1, M, L, O);
+  else if (parts <= 8)
     sq_merge_parts<8>(a, row, d0, p1, p2, 0, 1, M, L, O);
   else
     sq_merge_parts<16>(a, row, d0, p1, p2, 0, 1, M, L, O);
