@@ -106,6 +106,34 @@ __device__ __forceinline__ void load8(const SampleArgs& a, int row, int base, bo
   }
 }
 
+// log2 of the exponential noise E of elements base .. base+7 of a row: from
+// the caller's draw e[0..7] (NOISE), or from Philox at counter (offset +
+// base/4 + h, row) for h = 0, 1.
+template <bool NOISE>
+__device__ __forceinline__ void noise_log2(const SampleArgs& a, int row, int base, const float* e,
+                                           float* le) {
+  if constexpr (NOISE) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) le[i] = __builtin_amdgcn_logf(fmaxf(e[i], kMinNoise));
+  } else {
+    const uint32_t k0 = (uint32_t)a.seed, k1 = (uint32_t)(a.seed >> 32);
+    const uint64_t ctr = a.offset + (uint64_t)(base >> 2);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const U4 r = philox10(U4{(uint32_t)(ctr + h), (uint32_t)((ctr + h) >> 32), (uint32_t)row, 0u},
+                            k0, k1);
+      const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // u = (bits + 1) 2^-32 in (0, 1]; E / ln 2 = -log2(u), clamped like E >= 1e-10
+        const float u = ((float)w[j] + 1.0f) * 2.3283064365386963e-10f;
+        const float e2 = fmaxf(-__builtin_amdgcn_logf(u), kMinNoise * 1.4426950408889634f);
+        le[4 * h + j] = __builtin_amdgcn_logf(e2);
+      }
+    }
+  }
+}
+
 // Scores of one row chunk in log2 units: logits * log2(e) / T - log2(E)
 // (the base change and the constant log2(ln 2) of E = -ln u = -log2(u) ln 2
 // are common to every element of the row and do not move the maximiser).
@@ -113,47 +141,66 @@ template <typename T, bool NOISE>
 __global__ __launch_bounds__(kPartThreads) void sample_partial_kernel(SampleArgs a) {
   const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
   const float scale = NVK_LOG2E / a.temperatures[row];
-  const uint32_t k0 = (uint32_t)a.seed, k1 = (uint32_t)(a.seed >> 32);
   float best = -INFINITY;
   int best_i = 0x7fffffff;
+  if (sizeof(T) == 2 && a.vec_ok && (int64_t)(c + 1) * kChunk <= a.vocab) {
+    // a whole chunk of bf16: its logits (and the caller's noise) are all
+    // loaded before the first wait, so the loads overlap the Philox draw
+    const int64_t off = (int64_t)c * kChunk + tid * 8;
+    const uint16_t* p = static_cast<const uint16_t*>(a.logits) + (int64_t)row * a.row_stride + off;
+    nvk_u32x4 w[kIters];
 #pragma unroll
-  for (int it = 0; it < kIters; ++it) {
-    const int base = c * kChunk + (it * kPartThreads + tid) * 8;
-    if (base >= a.vocab) break;
-    const bool full = base + 8 <= a.vocab;
-    float l[8];
-    load8<T>(a, row, base, full, l);
-    float le[8];  // log2 of the noise
+    for (int it = 0; it < kIters; ++it)
+      w[it] = *reinterpret_cast<const nvk_u32x4*>(p + it * kPartThreads * 8);
+    float nz[NOISE ? kIters : 1][8];
     if constexpr (NOISE) {
-      const float* q = a.noise + (int64_t)row * a.noise_stride + base;
+      const float* q = a.noise + (int64_t)row * a.noise_stride + off;
+#pragma unroll
+      for (int it = 0; it < kIters; ++it)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) nz[it][i] = q[it * kPartThreads * 8 + i];
+    }
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const int base = c * kChunk + (it * kPartThreads + tid) * 8;
+      float le[8];
+      noise_log2<NOISE>(a, row, base, nz[NOISE ? it : 0], le);
+      const uint32_t ww[4] = {w[it].x, w[it].y, w[it].z, w[it].w};
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float e = (full || base + i < a.vocab) ? q[i] : 1.0f;
-        le[i] = __builtin_amdgcn_logf(fmaxf(e, kMinNoise));
-      }
-    } else {
-      const uint64_t ctr = a.offset + (uint64_t)(base >> 2);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const U4 r = philox10(U4{(uint32_t)(ctr + h), (uint32_t)((ctr + h) >> 32), (uint32_t)row, 0u},
-                              k0, k1);
-        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          // u = (bits + 1) 2^-32 in (0, 1]; E / ln 2 = -log2(u), clamped like E >= 1e-10
-          const float u = ((float)w[j] + 1.0f) * 2.3283064365386963e-10f;
-          const float e2 = fmaxf(-__builtin_amdgcn_logf(u), kMinNoise * 1.4426950408889634f);
-          le[4 * h + j] = __builtin_amdgcn_logf(e2);
+        const float l = (i & 1) ? nvk_bf16hi_to_f32(ww[i >> 1]) : nvk_bf16lo_to_f32(ww[i >> 1]);
+        const float sc = l * scale - le[i];
+        // a thread visits its indices in increasing order: strictly greater wins
+        if (sc > best) {
+          best = sc;
+          best_i = base + i;
         }
       }
     }
+  } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float sc = l[i] * scale - le[i];
-      // a thread visits its indices in increasing order: strictly greater wins
-      if (sc > best && (full || base + i < a.vocab)) {
-        best = sc;
-        best_i = base + i;
+    for (int it = 0; it < kIters; ++it) {
+      const int base = c * kChunk + (it * kPartThreads + tid) * 8;
+      if (base >= a.vocab) break;
+      const bool full = base + 8 <= a.vocab;
+      float l[8];
+      load8<T>(a, row, base, full, l);
+      float e[8];
+      if constexpr (NOISE) {
+        const float* q = a.noise + (int64_t)row * a.noise_stride + base;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] = (full || base + i < a.vocab) ? q[i] : 1.0f;
+      }
+      float le[8];
+      noise_log2<NOISE>(a, row, base, e, le);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float sc = l[i] * scale - le[i];
+        // a thread visits its indices in increasing order: strictly greater wins
+        if (sc > best && (full || base + i < a.vocab)) {
+          best = sc;
+          best_i = base + i;
+        }
       }
     }
   }
@@ -275,20 +322,41 @@ __global__ __launch_bounds__(kPartThreads) void sample_mass_kernel(SampleArgs a)
   const float scale = NVK_LOG2E / a.temperatures[row];
   float x[kIters][8];
   float mx = -INFINITY;
+  if (sizeof(T) == 2 && a.vec_ok && (int64_t)(c + 1) * kChunk <= a.vocab) {
+    // a whole chunk of bf16: the kIters 16-byte loads all leave before the
+    // first wait (the loop below waits for each in turn)
+    const uint16_t* p = static_cast<const uint16_t*>(a.logits) + (int64_t)row * a.row_stride +
+                        c * kChunk + tid * 8;
+    nvk_u32x4 w[kIters];
 #pragma unroll
-  for (int it = 0; it < kIters; ++it) {
-    const int base = c * kChunk + (it * kPartThreads + tid) * 8;
-    float l[8];
-    if (base < a.vocab) {
-      load8<T>(a, row, base, base + 8 <= a.vocab, l);
-    } else {
+    for (int it = 0; it < kIters; ++it)
+      w[it] = *reinterpret_cast<const nvk_u32x4*>(p + it * kPartThreads * 8);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) l[i] = -INFINITY;
+    for (int it = 0; it < kIters; ++it) {
+      const uint32_t ww[4] = {w[it].x, w[it].y, w[it].z, w[it].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[it][2 * i] = mass_x(nvk_bf16lo_to_f32(ww[i]), scale);
+        x[it][2 * i + 1] = mass_x(nvk_bf16hi_to_f32(ww[i]), scale);
+        mx = fmaxf(mx, fmaxf(x[it][2 * i], x[it][2 * i + 1]));
+      }
     }
+  } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      x[it][i] = mass_x(l[i], scale);
-      mx = fmaxf(mx, x[it][i]);
+    for (int it = 0; it < kIters; ++it) {
+      const int base = c * kChunk + (it * kPartThreads + tid) * 8;
+      float l[8];
+      if (base < a.vocab) {
+        load8<T>(a, row, base, base + 8 <= a.vocab, l);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) l[i] = -INFINITY;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        x[it][i] = mass_x(l[i], scale);
+        mx = fmaxf(mx, x[it][i]);
+      }
     }
   }
   const float M = block_max256(mx, red);
@@ -362,20 +430,39 @@ __global__ __launch_bounds__(256) void sample_pick_kernel(SampleArgs a) {
   float e[32];  // the thread's 32 elements, in index order
   float tsum = 0.f;
   const int first = pick * kChunk + 32 * tid;
+  if (sizeof(T) == 2 && a.vec_ok && first + 32 <= a.vocab) {
+    // 64 bf16 bytes: the four 16-byte loads leave before the first wait
+    const uint16_t* p = static_cast<const uint16_t*>(a.logits) + (int64_t)row * a.row_stride + first;
+    nvk_u32x4 w[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int base = first + 8 * j;
-    float l[8];
-    if (base < a.vocab) {
-      load8<T>(a, row, base, base + 8 <= a.vocab, l);
-    } else {
+    for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const nvk_u32x4*>(p + 8 * j);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) l[i] = -INFINITY;
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t ww[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        e[8 * j + 2 * i] = exp2f(mass_x(nvk_bf16lo_to_f32(ww[i]), scale) - Mc);
+        e[8 * j + 2 * i + 1] = exp2f(mass_x(nvk_bf16hi_to_f32(ww[i]), scale) - Mc);
+        tsum += e[8 * j + 2 * i];
+        tsum += e[8 * j + 2 * i + 1];
+      }
     }
+  } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      e[8 * j + i] = exp2f(mass_x(l[i], scale) - Mc);
-      tsum += e[8 * j + i];
+    for (int j = 0; j < 4; ++j) {
+      const int base = first + 8 * j;
+      float l[8];
+      if (base < a.vocab) {
+        load8<T>(a, row, base, base + 8 <= a.vocab, l);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) l[i] = -INFINITY;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        e[8 * j + i] = exp2f(mass_x(l[i], scale) - Mc);
+        tsum += e[8 * j + i];
+      }
     }
   }
   float tot;
