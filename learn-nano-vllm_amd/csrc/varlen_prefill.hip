@@ -86,6 +86,7 @@ struct PrefillArgs {
 };
 
 constexpr int kRecFloats = HD + 4;  // partial record of one row: O[HD], m, l, pad
+constexpr int kMaxSplits = 16;      // key-range splits of one query tile
 
 // ---- longest-first order of the query tiles ----------------------------------
 // The hardware starts workgroups in blockIdx order as slots free up.  Ranking
@@ -760,14 +761,19 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
 }
 
 // Merges the split-K partial records of one (sequence, kv head, query tile):
-// thread t handles row t/2 and d range 64*(t%2) .. +63.
+// thread t handles row t/8 and d range 16*(t%8) .. +15.  The m of every live
+// split is fetched in one round trip, then the splits are folded in order,
+// kFoldBatch at a time with all their loads in flight (left to itself the
+// compiler waits for each split's m in turn and keeps four of a split's
+// loads in flight).
+constexpr int kFoldBatch = 4;
 template <int G, int MODE, bool F16>
-__global__ __launch_bounds__(2 * kRows) void prefill_combine_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(8 * kRows) void prefill_combine_kernel(PrefillArgs a) {
   constexpr int TQ = kRows / G;
   const int kvh = blockIdx.x, s = blockIdx.y, qt = blockIdx.z;
   const QTile qi = qtile_info<MODE>(a, s, qt, TQ);
   if (!qi.live) return;
-  const int r = threadIdx.x >> 1, dh = threadIdx.x & 1;
+  const int r = threadIdx.x >> 3, dq = threadIdx.x & 7;
   const int tok = qi.q0 + r / G;
   if (tok < 0 || tok >= qi.Lq) return;
   const int head = kvh * G + r % G;
@@ -779,28 +785,48 @@ __global__ __launch_bounds__(2 * kRows) void prefill_combine_kernel(PrefillArgs 
                                  a.n_splits * (int64_t)kRows * kRecFloats +
                       (int64_t)r * kRecFloats;
   const int64_t split_stride = (int64_t)kRows * kRecFloats;
+  float mv[kMaxSplits];
+#pragma unroll
+  for (int j = 0; j < kMaxSplits; ++j) {
+    const float m = rec0[(j < n_live ? j : 0) * split_stride + HD];
+    mv[j] = j < n_live ? m : -INFINITY;
+  }
   float M = -INFINITY;
-  for (int j = 0; j < n_live; ++j) M = fmaxf(M, rec0[j * split_stride + HD]);
+#pragma unroll
+  for (int j = 0; j < kMaxSplits; ++j) M = fmaxf(M, mv[j]);
   float L = 0.f;
-  nvk_f32x4 acc[16];
+  nvk_f32x4 acc[4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = nvk_f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < n_live; ++j) {
-    const float* rec = rec0 + j * split_stride;
-    const float m = rec[HD];
-    const float w = m == -INFINITY ? 0.f : nvk_fast_exp2(m - M);
-    L += w * rec[HD + 1];
+  for (int i = 0; i < 4; ++i) acc[i] = nvk_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const nvk_f32x4 o = *reinterpret_cast<const nvk_f32x4*>(rec + 64 * dh + 4 * i);
-      acc[i] += w * o;
+  for (int j0 = 0; j0 < kMaxSplits; j0 += kFoldBatch) {
+    if (j0 >= n_live) break;
+    float lv[kFoldBatch];
+    nvk_f32x4 ov[kFoldBatch][4];
+#pragma unroll
+    for (int u = 0; u < kFoldBatch; ++u) {
+      const int j = j0 + u < n_live ? j0 + u : j0;  // past the last live split: reread j0, weight 0
+      const float* rec = rec0 + j * split_stride;
+      lv[u] = rec[HD + 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ov[u][i] = *reinterpret_cast<const nvk_f32x4*>(rec + 16 * dq + 4 * i);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kFoldBatch; ++u) {
+      if (j0 + u >= n_live) break;
+      const float m = mv[j0 + u];
+      const float w = m == -INFINITY ? 0.f : nvk_fast_exp2(m - M);
+      L += w * lv[u];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] += w * ov[u][i];
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   uint16_t* op = a.out + ((int64_t)qi.q_row0 + tok) * a.out_stride_tok +
-                 (int64_t)head * a.out_stride_head + 64 * dh;
+                 (int64_t)head * a.out_stride_head + 16 * dq;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {  // 8-byte stores: out is only required 8-byte aligned
+  for (int i = 0; i < 4; ++i) {  // 8-byte stores: out is only required 8-byte aligned
     nvk_u32x2 w;
     w.x = NvkElt<F16>::pack2(acc[i][0] * inv, acc[i][1] * inv);
     w.y = NvkElt<F16>::pack2(acc[i][2] * inv, acc[i][3] * inv);
@@ -817,7 +843,7 @@ int launch_mode(const PrefillArgs& a, hipStream_t stream) {
     const int st = nvk_launch_status();
     if (st != NVK_OK) return st;
     dim3 cgrid(a.num_kv_heads, a.batch, a.n_qtiles);
-    hipLaunchKernelGGL((prefill_combine_kernel<G, MODE, F16>), cgrid, dim3(2 * kRows), 0, stream,
+    hipLaunchKernelGGL((prefill_combine_kernel<G, MODE, F16>), cgrid, dim3(8 * kRows), 0, stream,
                        a);
   }
   return nvk_launch_status();
@@ -858,7 +884,7 @@ static SplitPlan plan_splits(int batch, int max_seqlen_q, int64_t max_keys, int 
   p.n_splits = 1;
   const int64_t max_tiles = (max_keys + kKeys - 1) / kKeys;
   const int64_t wgs = (int64_t)num_kv_heads * batch * p.n_qtiles;
-  constexpr int64_t kTargetWgs = 1024, kMinTilesPerSplit = 8, kMaxSplits = 16;
+  constexpr int64_t kTargetWgs = 1024, kMinTilesPerSplit = 8;
   if (wgs > 0 && wgs < kTargetWgs && max_tiles >= 2 * kMinTilesPerSplit &&
       2 * max_seqlen_q <= TQ) {
     int64_t n = (kTargetWgs + wgs - 1) / wgs;
