@@ -58,6 +58,21 @@ def test_sampler_padded_row_stride():
     _check_tokens(tok, bits(logits.cpu()), temps.numpy(), noise.numpy())
 
 
+def test_sampler_whole_chunks_with_unaligned_noise_rows():
+    """Logits rows 16-byte aligned (a padded view) over two whole 8192-token
+    chunks plus 5 tokens, the caller's noise contiguous with an odd row length,
+    so every other noise row starts 4 bytes past a 16-byte boundary."""
+    say("sampler whole chunks, unaligned noise rows")
+    g = torch.Generator().manual_seed(5)
+    v = 2 * 8192 + 5
+    full = (torch.randn(6, 16400, generator=g) * 2).to(torch.bfloat16).cuda()
+    logits = full[:, :v]
+    temps = (0.5 + torch.rand(6, generator=g)).to(torch.float32)
+    noise = torch.empty(6, v).exponential_(1.0, generator=g)
+    tok = Sampler()(logits, temps.cuda(), noise=noise.cuda()).cpu().numpy()
+    _check_tokens(tok, bits(logits.cpu()), temps.numpy(), noise.numpy())
+
+
 def _raw_sample(logits, temps, seed, offset):
     lib = _lib.load()
     out = torch.empty(logits.shape[0], dtype=torch.int64, device="cuda")
