@@ -134,6 +134,9 @@ def test_fp16_needles_decode_prefill_short_query():
     # 32 x 6 over contexts up to 8192: the short-query kernel with K staged in LDS
     lk = [int(x) for x in rng.integers(1024, 8193, 32)]
     run_schedule(NeedleCase(100, [6] * 32, lk, dtype=F16), pre, 64, "fp16 short query, K in LDS")
+    # 2 x 6 over long contexts: every group cut into ~64 parts, sliced combine
+    run_schedule(NeedleCase(101, [6] * 2, [9000, 12000], dtype=F16), pre, 64,
+                 "fp16 short query, sliced combine")
 
 
 def test_fp16_noalloc_decode_matches_workspace_decode():
