@@ -246,6 +246,17 @@ __device__ __forceinline__ void lds_load_buffer(const nvk_u32x4& rsrc, uint32_t 
   asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :: "v"(voffset), "s"(rsrc), "s"(dst) : "memory", "m0");
 }
+// The same with the LDS address dst + J KiB formed in M0 by one scalar add.
+template <int J>
+__device__ __forceinline__ void lds_load_buffer_at(const nvk_u32x4& rsrc, uint32_t voffset,
+                                                   uint32_t dst) {
+  if constexpr (J == 0)
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :: "v"(voffset), "s"(rsrc), "s"(dst) : "memory", "m0");
+  else
+    asm volatile("s_add_u32 m0, %2, %3\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :: "v"(voffset), "s"(rsrc), "s"(dst), "n"(J * 1024) : "memory", "m0", "scc");
+}
 // readfirstlane of wave-uniform values the compiler may have computed with
 // vector instructions (inline asm "s" operands need SGPRs).
 __device__ __forceinline__ uint32_t uniform(uint32_t x) {
@@ -337,6 +348,12 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
   const uint32_t v_row_bytes =
       MODE == kDense ? (uint32_t)a.v_stride_tok * 2u : (uint32_t)a.num_kv_heads * HD * 2u;
   const int64_t paged_row_elems = (int64_t)a.num_kv_heads * HD;
+  // Aligned paged mode: the kv head's first element in page 0 and the page
+  // stride in bytes (below 2^32, checked at launch), so a tile's address is
+  // one 32 x 32 -> 64-bit product and two adds.
+  const uint64_t head_k = (uint64_t)(uintptr_t)(a.k + kvh * HD);
+  const uint64_t head_v = (uint64_t)(uintptr_t)(a.v + kvh * HD);
+  const uint32_t page_bytes = (uint32_t)a.block_size * k_row_bytes;
   // kPagedAny: a key that does not exist reads the sequence's first q row
   // (finite); its score is masked to -inf and its probability is 0.
   const uint16_t* dummy = a.q + (int64_t)q_row0 * a.q_stride_tok;
@@ -379,27 +396,35 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
                      8 * dma_chunk(j);
       }
     } else {
-      const uint16_t* tb;
       uint32_t bytes = (uint32_t)rem * (is_v ? v_row_bytes : k_row_bytes);
+      nvk_u32x4 r;
       if constexpr (MODE == kDense) {
-        tb = src + (int64_t)(k_row0 + base) * (is_v ? a.v_stride_tok : a.k_stride_tok) +
-             (int64_t)kvh * a.kv_stride_head;
+        const uint16_t* tb = src + (int64_t)(k_row0 + base) * (is_v ? a.v_stride_tok : a.k_stride_tok) +
+                             (int64_t)kvh * a.kv_stride_head;
+        r = tile_rsrc(tb, bytes);
       } else {
         const bool ok = (uint32_t)page < (uint32_t)a.num_blocks;
-        const int64_t prow = ok ? (int64_t)page * a.block_size + in_page : 0;  // no branch
-        tb = src + prow * paged_row_elems + kvh * HD;
-        bytes = ok ? bytes : 0u;
+        const uint64_t off = (uint64_t)(uint32_t)page * page_bytes + (uint32_t)in_page * k_row_bytes;
+        const uint64_t b = (is_v ? head_v : head_k) + (ok ? off : 0);  // no branch
+        r = nvk_u32x4{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, ok ? bytes : 0u, 0x00020000u};
       }
-      const nvk_u32x4 r = tile_rsrc(tb, bytes);
       pl.rsrc = nvk_u32x4{uniform(r.x), uniform(r.y), uniform(r.z), uniform(r.w)};
     }
     return pl;
   };
+  static_assert(4 * kRowBytes == 1024 && kLoadsPerWave <= 4, "load j lands at dst0 + j KiB");
   auto issue_load = [&](const DmaPlan& pl, int j, bool is_v) {
-    if constexpr (MODE == kPagedAny)
+    if constexpr (MODE == kPagedAny) {
       lds_load_global(pl.rows[j], pl.dst0 + 4 * j * kRowBytes);
-    else
-      lds_load_buffer(pl.rsrc, is_v ? v_voff[j] : k_voff[j], pl.dst0 + 4 * j * kRowBytes);
+    } else {
+      const uint32_t vo = is_v ? v_voff[j] : k_voff[j];
+      switch (j) {  // j is a constant wherever the loop schedule is unrolled
+        case 0: lds_load_buffer_at<0>(pl.rsrc, vo, pl.dst0); break;
+        case 1: lds_load_buffer_at<1>(pl.rsrc, vo, pl.dst0); break;
+        case 2: lds_load_buffer_at<2>(pl.rsrc, vo, pl.dst0); break;
+        default: lds_load_buffer_at<3>(pl.rsrc, vo, pl.dst0); break;
+      }
+    }
   };
 
   // Page ids (kPagedAligned): read one step before the tile's load is issued.
@@ -852,7 +877,10 @@ int launch_mode(const PrefillArgs& a, hipStream_t stream) {
 template <int G, bool F16>
 int launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   if (!a.block_tables) return launch_mode<G, kDense, F16>(a, stream);
-  if (a.block_size % kKeys == 0) return launch_mode<G, kPagedAligned, F16>(a, stream);
+  // aligned pages whose byte size fits 32 bits (tile addresses in 32 x 32-bit products)
+  if (a.block_size % kKeys == 0 &&
+      (uint64_t)a.block_size * a.num_kv_heads * HD * 2 <= UINT32_MAX)
+    return launch_mode<G, kPagedAligned, F16>(a, stream);
   return launch_mode<G, kPagedAny, F16>(a, stream);
 }
 
