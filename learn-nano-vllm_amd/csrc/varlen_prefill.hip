@@ -33,6 +33,8 @@
 //     v_dot2_f32_bf16 over the packed probabilities.
 //   * The grid runs the query tiles nearest the end of each sequence (the
 //     ones with most keys) first.
+#include <type_traits>
+
 #include "nvk_common.h"
 #include "short_query.h"
 
@@ -453,18 +455,22 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
   const int k_swz = swz(l32);
   const uint32_t k_addr0 = lds_addr(lds) + l32 * kRowBytes + 16 * ((half ^ k_swz) & 1) +
                            32 * (k_swz >> 1);
-  auto compute_s = [&](int stage, nvk_f32x16 (&acc)[2]) {
-    uint32_t ka = k_addr0 + stage * kTileBytes;
-    asm volatile("" : "+v"(ka));  // rebuilt every tile: keeps 8 addresses out of registers
+  // The XOR touches bits 5-7 only and the stage / block offsets are multiples
+  // of 8 KiB, so the address of fragment ks in stage st, block mb is
+  // k_addr[ks] + st * kTileBytes + 8192 mb: a constant offset of the read.
+  uint32_t k_addr[HD / 16];
+#pragma unroll
+  for (int ks = 0; ks < HD / 16; ++ks) k_addr[ks] = k_addr0 ^ (32u * ks);
+  auto compute_s = [&](auto stage, nvk_f32x16 (&acc)[2]) {
+    constexpr int ST = decltype(stage)::value;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) acc[mb] = nvk_f32x16{};
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) {
-      const uint32_t addr = ka ^ (32u * ks);
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
         const vec8 kf = *reinterpret_cast<const __attribute__((address_space(3))) vec8*>(
-            (size_t)(addr + 32 * kRowBytes * mb));
+            (size_t)(k_addr[ks] + ST * kTileBytes + 32 * kRowBytes * mb));
         acc[mb] = E::mfma32x32x16(kf, qf[ks], acc[mb]);
       }
     }
@@ -489,6 +495,14 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     v_lo0 = v0 + (4 * half + tr_key) * kRowBytes + 16 * (tr_c0 ^ (sw_lo & 3)) + 64 * (sw_lo >> 2);
     v_hi0 = v0 + (8 + 4 * half + tr_key) * kRowBytes + 16 * (tr_c0 ^ (sw_hi & 3)) +
             64 * (sw_hi >> 2);
+  }
+  // V read addresses of d block db in stage 0 (bits 6-7 XORed; stage and k-step
+  // offsets are multiples of 4 KiB and become constant offsets of the reads)
+  uint32_t v_lo[HD / 32], v_hi[HD / 32];
+#pragma unroll
+  for (int db = 0; db < HD / 32; ++db) {
+    v_lo[db] = v_lo0 ^ (64u * db);
+    v_hi[db] = v_hi0 ^ (64u * db);
   }
   // Online softmax in log2 units with a lazily updated reference max: the
   // probabilities are exp2(score - m_ref) with m_ref at most kLazy below the
@@ -566,22 +580,23 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
   // Between the MFMAs: the loads of V(kt+1) and K(kt+2) and, in SALU, the
   // plans of the next step's loads (V(kt+2), K(kt+3); pages pg_v / pg_k).
   // LDS operands are read two MFMAs ahead.
-  auto mma_step = [&](int kt, nvk_f32x16 (&sc)[2], float moff, const DmaPlan& plan_v,
+  // Stages: tile t sits in stage (t - t_begin) & 1, so the step loop runs
+  // two steps per pass and every stage offset is a constant (P: the stage of
+  // tile kt).
+  auto mma_step = [&](auto par, int kt, nvk_f32x16 (&sc)[2], float moff, const DmaPlan& plan_v,
                       const DmaPlan& plan_k, int pg_v, int ip_v, int pg_k, int ip_k,
                       DmaPlan& next_v, DmaPlan& next_k, float& mt_next) {
-    uint32_t ka = k_addr0 + ((kt + 1) & 1) * kTileBytes;
-    uint32_t va_lo = v_lo0 + (kt & 1) * kTileBytes, va_hi = v_hi0 + (kt & 1) * kTileBytes;
-    asm volatile("" : "+v"(ka), "+v"(va_lo), "+v"(va_hi));  // rebuilt per step
-    auto rd_k = [&](int ks, int mb) {
+    constexpr int P = decltype(par)::value;
+    auto rd_k = [&](int ks, int mb) {  // K of tile kt+1
       return *reinterpret_cast<const __attribute__((address_space(3))) vec8*>(
-          (size_t)((ka ^ (32u * ks)) + 32 * kRowBytes * mb));
+          (size_t)(k_addr[ks] + (1 - P) * kTileBytes + 32 * kRowBytes * mb));
     };
-    auto rd_v = [&](int db, int ks) {
+    auto rd_v = [&](int db, int ks) {  // V of tile kt
       const nvk_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) nvk_i16x4*)(size_t)((va_lo ^ (64u * db)) +
+          (__attribute__((address_space(3))) nvk_i16x4*)(size_t)(v_lo[db] + P * kTileBytes +
                                                                   16 * ks * kRowBytes));
       const nvk_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) nvk_i16x4*)(size_t)((va_hi ^ (64u * db)) +
+          (__attribute__((address_space(3))) nvk_i16x4*)(size_t)(v_hi[db] + P * kTileBytes +
                                                                   16 * ks * kRowBytes));
       const nvk_i16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       return __builtin_bit_cast(vec8, w);
@@ -648,9 +663,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
         const int j = k_load_at(8 * mb + ks);
         if (j >= 0) issue_load(plan_k, j, false);
         if constexpr (MODE != kPagedAny) {
-          if (mb == 0 && ks == 5) next_v = plan_tile(kt + 2, v_stage(kt & 1), true, pg_v, ip_v);
+          if (mb == 0 && ks == 5) next_v = plan_tile(kt + 2, v_stage(P), true, pg_v, ip_v);
           if (mb == 1 && ks == 1)
-            next_k = plan_tile(kt + 3, k_stage((kt + 1) & 1), false, pg_k, ip_k);
+            next_k = plan_tile(kt + 3, k_stage(1 - P), false, pg_k, ip_k);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -698,9 +713,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     }
     auto next_in_page = [&](int x) { return x + kKeys == a.block_size ? 0 : x + kKeys; };
     {
-      const DmaPlan k0 = plan_tile(tb, k_stage(tb & 1), false, pg[0], ip[0]);
-      const DmaPlan v0 = plan_tile(tb, v_stage(tb & 1), true, pg[0], ip[0]);
-      const DmaPlan k1 = plan_tile(tb + 1, k_stage((tb + 1) & 1), false, pg[1], ip[1]);
+      const DmaPlan k0 = plan_tile(tb, k_stage(0), false, pg[0], ip[0]);
+      const DmaPlan v0 = plan_tile(tb, v_stage(0), true, pg[0], ip[0]);
+      const DmaPlan k1 = plan_tile(tb + 1, k_stage(1), false, pg[1], ip[1]);
 #pragma unroll
       for (int j = 0; j < kLoadsPerWave; ++j) {
         issue_load(k0, j, false);
@@ -708,13 +723,13 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
         issue_load(k1, j, false);
       }
     }
-    DmaPlan plan_v = plan_tile(tb + 1, v_stage((tb + 1) & 1), true, pg[1], ip[1]);
-    DmaPlan plan_k = plan_tile(tb + 2, k_stage(tb & 1), false, pg[2], ip[2]);
+    DmaPlan plan_v = plan_tile(tb + 1, v_stage(1), true, pg[1], ip[1]);
+    DmaPlan plan_k = plan_tile(tb + 2, k_stage(0), false, pg[2], ip[2]);
     int page_a = pg[2], page_b = pg[3];  // pages of tiles kt+2, kt+3
     int ip_a = ip[2], ip_b = ip[3];
     wait_lds_loads();
     __syncthreads();
-    compute_s(tb & 1, sc);
+    compute_s(std::integral_constant<int, 0>{}, sc);
     mask_tile(sc, tb);
     float mt;
     {
@@ -723,7 +738,8 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       for (int st = 0; st < 15; ++st) mx = max_step(sc, mx, st);
       mt = max_finish(sc, mx);
     }
-    for (int kt = tb; kt < t_end; ++kt) {
+    auto step = [&](auto par, int kt) {
+      constexpr int P = decltype(par)::value;
       wait_lds_loads();
       __syncthreads();
       int page_c = 0;
@@ -733,19 +749,25 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
         if (kt + 4 < t_end) page_c = fetch_page(kt + 4);
       }
       if constexpr (MODE == kPagedAny) {
-        plan_v = plan_tile(kt + 1, v_stage((kt + 1) & 1), true, 0, 0);
-        plan_k = plan_tile(kt + 2, k_stage(kt & 1), false, 0, 0);
+        plan_v = plan_tile(kt + 1, v_stage(1 - P), true, 0, 0);
+        plan_k = plan_tile(kt + 2, k_stage(P), false, 0, 0);
       }
       const float moff = rescale(mt);
       DmaPlan next_v = plan_v, next_k = plan_k;
-      mma_step(kt, sc, moff, plan_v, plan_k, page_a, ip_a, page_b, ip_b, next_v, next_k, mt);
+      mma_step(par, kt, sc, moff, plan_v, plan_k, page_a, ip_a, page_b, ip_b, next_v, next_k, mt);
       plan_v = next_v;
       plan_k = next_k;
       page_a = page_b;
       page_b = page_c;
       ip_a = ip_b;
       ip_b = next_in_page(ip_b);
+    };
+    int kt = tb;
+    for (; kt + 1 < t_end; kt += 2) {
+      step(std::integral_constant<int, 0>{}, kt);
+      step(std::integral_constant<int, 1>{}, kt + 1);
     }
+    if (kt < t_end) step(std::integral_constant<int, 0>{}, kt);
   }
 
   // ---- epilogue: normalise and store the row -----------------------------------
