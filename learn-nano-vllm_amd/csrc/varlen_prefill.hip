@@ -243,12 +243,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // `rsrc`: a raw buffer descriptor (wave-uniform); loads at offsets >= its
 // size write zeros.
 // `rsrc` and `dst` must be wave-uniform values held in SGPRs (see uniform()).
-__device__ __forceinline__ void lds_load_buffer(const nvk_u32x4& rsrc, uint32_t voffset,
-                                                uint32_t dst) {
-  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :: "v"(voffset), "s"(rsrc), "s"(dst) : "memory", "m0");
-}
-// The same with the LDS address dst + J KiB formed in M0 by one scalar add.
+// Load 16 bytes per lane from the buffer `rsrc` at byte `voffset` into LDS at
+// dst + J KiB + 16 * lane (the LDS address formed in M0 by one scalar op).
 template <int J>
 __device__ __forceinline__ void lds_load_buffer_at(const nvk_u32x4& rsrc, uint32_t voffset,
                                                    uint32_t dst) {
@@ -412,6 +408,32 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       }
       pl.rsrc = nvk_u32x4{uniform(r.x), uniform(r.y), uniform(r.z), uniform(r.w)};
     }
+    return pl;
+  };
+  // Aligned paged mode: a tile's byte offset from the kv head's first element
+  // of page 0 and its byte count (both 0 when the page id is outside the
+  // pool; 0 bytes past the tile range).  K and V rows share them, so each
+  // step computes one (the K tile's) and the next step's V plan reuses it.
+  struct TileOff {
+    uint64_t off;
+    uint32_t bytes;
+  };
+  auto tile_off = [&](int kt, int page, int in_page) {
+    const int base = kt * kKeys;
+    int rem = n_keys - base < kKeys ? n_keys - base : kKeys;
+    rem = (rem > 0 && kt < t_end) ? rem : 0;
+    const bool ok = (uint32_t)page < (uint32_t)a.num_blocks;
+    TileOff t;
+    t.off = ok ? (uint64_t)(uint32_t)page * page_bytes + (uint32_t)in_page * k_row_bytes : 0;
+    t.bytes = ok ? (uint32_t)rem * k_row_bytes : 0u;
+    return t;
+  };
+  auto plan_at = [&](const TileOff& t, uint8_t* dst, bool is_v) {
+    DmaPlan pl;
+    pl.dst0 = uniform(lds_addr(dst + kTileRowsPerWave * wave * kRowBytes));
+    const uint64_t b = (is_v ? head_v : head_k) + t.off;
+    pl.rsrc = nvk_u32x4{uniform((uint32_t)b), uniform((uint32_t)(b >> 32) & 0xFFFFu),
+                        uniform(t.bytes), 0x00020000u};
     return pl;
   };
   static_assert(4 * kRowBytes == 1024 && kLoadsPerWave <= 4, "load j lands at dst0 + j KiB");
@@ -585,7 +607,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
   // tile kt).
   auto mma_step = [&](auto par, int kt, nvk_f32x16 (&sc)[2], float moff, const DmaPlan& plan_v,
                       const DmaPlan& plan_k, int pg_v, int ip_v, int pg_k, int ip_k,
-                      DmaPlan& next_v, DmaPlan& next_k, float& mt_next) {
+                      DmaPlan& next_v, DmaPlan& next_k, float& mt_next, TileOff& toff) {
     constexpr int P = decltype(par)::value;
     auto rd_k = [&](int ks, int mb) {  // K of tile kt+1
       return *reinterpret_cast<const __attribute__((address_space(3))) vec8*>(
@@ -662,7 +684,13 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
         }
         const int j = k_load_at(8 * mb + ks);
         if (j >= 0) issue_load(plan_k, j, false);
-        if constexpr (MODE != kPagedAny) {
+        if constexpr (MODE == kPagedAligned) {  // toff: tile kt+2 in, tile kt+3 out
+          if (mb == 0 && ks == 5) next_v = plan_at(toff, v_stage(P), true);
+          if (mb == 1 && ks == 1) {
+            toff = tile_off(kt + 3, pg_k, ip_k);
+            next_k = plan_at(toff, k_stage(1 - P), false);
+          }
+        } else if constexpr (MODE == kDense) {
           if (mb == 0 && ks == 5) next_v = plan_tile(kt + 2, v_stage(P), true, pg_v, ip_v);
           if (mb == 1 && ks == 1)
             next_k = plan_tile(kt + 3, k_stage(1 - P), false, pg_k, ip_k);
@@ -724,7 +752,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       }
     }
     DmaPlan plan_v = plan_tile(tb + 1, v_stage(1), true, pg[1], ip[1]);
-    DmaPlan plan_k = plan_tile(tb + 2, k_stage(0), false, pg[2], ip[2]);
+    TileOff toff = tile_off(tb + 2, pg[2], ip[2]);  // aligned paged: tile kt+2 of the step
+    DmaPlan plan_k = MODE == kPagedAligned ? plan_at(toff, k_stage(0), false)
+                                           : plan_tile(tb + 2, k_stage(0), false, pg[2], ip[2]);
     int page_a = pg[2], page_b = pg[3];  // pages of tiles kt+2, kt+3
     int ip_a = ip[2], ip_b = ip[3];
     wait_lds_loads();
@@ -754,7 +784,8 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       }
       const float moff = rescale(mt);
       DmaPlan next_v = plan_v, next_k = plan_k;
-      mma_step(par, kt, sc, moff, plan_v, plan_k, page_a, ip_a, page_b, ip_b, next_v, next_k, mt);
+      mma_step(par, kt, sc, moff, plan_v, plan_k, page_a, ip_a, page_b, ip_b, next_v, next_k, mt,
+               toff);
       plan_v = next_v;
       plan_k = next_k;
       page_a = page_b;
