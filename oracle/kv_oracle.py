@@ -1,8 +1,8 @@
 """CPU oracle of the nano-vLLM KV-cache hot path.
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py may import this module, and only as the checker
-or the timed CPU baseline.  The product (learn-nano-vllm_amd/nanovllm_amd and
+cpu_baseline leg of bench.py may import this module, and only as the parity
+reference or the timed CPU baseline.  The product (learn-nano-vllm_amd/nanovllm_amd and
 libnvk.so) never calls it: there is no CPU fallback.
 
 What it restates (numpy, bf16 carried as uint16 bit patterns):

@@ -1,7 +1,7 @@
 """Host restatement of the reference's attention-metadata builders.
 
 TEST INFRASTRUCTURE ONLY, like the rest of oracle/: tests/ and the
-cpu_baseline leg of bench.py use it as the checker of the device builders
+cpu_baseline leg of bench.py use it as the parity reference of the device builders
 (nanovllm_amd/engine/device_metadata.py) and as the timed host path; the
 product never imports it.
 
