@@ -97,6 +97,21 @@ def test_decode_zero_context_rows_write_zeros():
     assert_attn_close(out, ref, "zero-context")
 
 
+def test_decode_zero_context_row_beside_a_long_context():
+    """An empty context next to one of 16000 keys: the grid has far more than
+    32 waves per group, so the sliced combine writes the zero rows."""
+    case = decode_case(seed=13, ctx=[0, 16000], pool_blocks=70)
+    c = case.to("cuda")
+    out = torch.full((2, 16, 128), 7.0, dtype=torch.bfloat16, device="cuda")
+    say("decode zero-context row, sliced combine")
+    paged_decode(c.q, c.k_cache, c.v_cache, c.context_lens, c.block_tables, case.scale, out=out)
+    torch.cuda.synchronize()
+    assert out[0].eq(0).all()
+    ref = oracle_decode(case.q, case.k_cache, case.v_cache, case.block_tables, case.context_lens,
+                        256, case.scale)
+    assert_attn_close(out, ref, "zero-context beside 16000 keys")
+
+
 def test_decode_strided_query_and_flash_api_shape():
     case = decode_case(seed=13, ctx=[100, 2000, 37], pool_blocks=12)
     c = case.to("cuda")
