@@ -391,6 +391,25 @@ int nvk_decode_metadata(const int32_t* seq_lens, const int32_t* bt_offsets,
                         int32_t* block_tables, void* stream);
 
 /*
+ * Refresh of a captured decode graph's static metadata before a replay, the
+ * copies of ModelRunner.run_model (nanovllm/engine/model_runner.py:200-211)
+ * in one kernel: for b < static_rows
+ *   slot_mapping[b] = b < batch ? src_slot_mapping[b] : -1,
+ *   context_lens[b] = b < batch ? src_context_lens[b] : 0,
+ *   positions[b]    = src_positions[b] for b < batch (rows above untouched),
+ * and block_tables[b][j] = src_block_tables[b][j] for b < batch, j < width
+ * (row strides bt_stride / src_bt_stride; everything else untouched, as the
+ * reference leaves it).  batch <= static_rows.  Nothing allocated,
+ * asynchronous on `stream`.
+ */
+int nvk_decode_graph_refresh(const int64_t* src_positions, const int32_t* src_slot_mapping,
+                             const int32_t* src_context_lens, const int32_t* src_block_tables,
+                             int64_t src_bt_stride, int32_t batch, int32_t width,
+                             int64_t* positions, int32_t* slot_mapping, int32_t* context_lens,
+                             int32_t* block_tables, int64_t bt_stride, int32_t static_rows,
+                             void* stream);
+
+/*
  * cu_seqlens of a query block of seqlen_q tokens at the end of every
  * sequence's seqlens_k[b] keys (speculative-decode verification through
  * flash_attn_with_kvcache with seqlen_q > 1, whose cache_seqlens

@@ -167,6 +167,42 @@ __global__ __launch_bounds__(kThreads) void uniform_cu_seqlens_kernel(const int3
   }
 }
 
+// Refresh of a captured decode graph's static metadata: slot -1 and context 0
+// past the live batch up to the static rows, the live block-table rectangle
+// copied (the rest of the table left as it is).
+struct GraphRefreshArgs {
+  const int64_t* src_pos;
+  const int32_t* src_slot;
+  const int32_t* src_ctx;
+  const int32_t* src_bt;
+  int64_t src_bt_stride;
+  int batch, width, static_rows;
+  int64_t* pos;
+  int32_t* slot;
+  int32_t* ctx;
+  int32_t* bt;
+  int64_t bt_stride;
+};
+
+__global__ __launch_bounds__(kThreads) void decode_graph_refresh_kernel(GraphRefreshArgs a) {
+  const int64_t cells = (int64_t)a.batch * a.width;
+  const int64_t n = cells > a.static_rows ? cells : a.static_rows;
+  for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * kThreads) {
+    if (e < a.static_rows) {
+      const int b = (int)e;
+      const bool live = b < a.batch;
+      a.slot[b] = live ? a.src_slot[b] : -1;
+      a.ctx[b] = live ? a.src_ctx[b] : 0;
+      if (live) a.pos[b] = a.src_pos[b];
+    }
+    if (e < cells) {
+      const int64_t b = e / a.width, j = e - b * a.width;
+      a.bt[b * a.bt_stride + j] = a.src_bt[b * a.src_bt_stride + j];
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" int nvk_prefill_metadata(const int32_t* num_cached, const int32_t* num_new,
@@ -247,5 +283,44 @@ extern "C" int nvk_uniform_cu_seqlens(const int32_t* seqlens_k, int32_t batch, i
   hipLaunchKernelGGL(uniform_cu_seqlens_kernel, dim3(1), dim3(kThreads), 0,
                      reinterpret_cast<hipStream_t>(stream), seqlens_k, batch, seqlen_q,
                      cu_seqlens_q, cu_seqlens_k);
+  return nvk_launch_status();
+}
+
+extern "C" int nvk_decode_graph_refresh(const int64_t* src_positions,
+                                        const int32_t* src_slot_mapping,
+                                        const int32_t* src_context_lens,
+                                        const int32_t* src_block_tables, int64_t src_bt_stride,
+                                        int32_t batch, int32_t width, int64_t* positions,
+                                        int32_t* slot_mapping, int32_t* context_lens,
+                                        int32_t* block_tables, int64_t bt_stride,
+                                        int32_t static_rows, void* stream) {
+  if (batch < 0 || width < 0 || static_rows < 0 || batch > static_rows) return NVK_EINVAL;
+  if (static_rows == 0) return NVK_OK;
+  if (!positions || !slot_mapping || !context_lens) return NVK_EINVAL;
+  if (batch > 0 && (!src_positions || !src_slot_mapping || !src_context_lens)) return NVK_EINVAL;
+  if (batch > 0 && width > 0) {
+    if (!src_block_tables || !block_tables) return NVK_EINVAL;
+    if (src_bt_stride < width || bt_stride < width) return NVK_EINVAL;
+  }
+  GraphRefreshArgs a;
+  a.src_pos = src_positions;
+  a.src_slot = src_slot_mapping;
+  a.src_ctx = src_context_lens;
+  a.src_bt = src_block_tables;
+  a.src_bt_stride = src_bt_stride;
+  a.batch = batch;
+  a.width = batch > 0 ? width : 0;
+  a.static_rows = static_rows;
+  a.pos = positions;
+  a.slot = slot_mapping;
+  a.ctx = context_lens;
+  a.bt = block_tables;
+  a.bt_stride = bt_stride;
+  const int64_t cells = (int64_t)a.batch * a.width;
+  const int64_t n = cells > static_rows ? cells : static_rows;
+  int64_t grid = (n + kThreads - 1) / kThreads;
+  grid = grid > kMaxGrid ? kMaxGrid : grid;
+  hipLaunchKernelGGL(decode_graph_refresh_kernel, dim3((unsigned)grid), dim3(kThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
   return nvk_launch_status();
 }

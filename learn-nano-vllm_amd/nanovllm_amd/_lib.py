@@ -75,6 +75,9 @@ SIGNATURES = {
                                             _c_ptr]),
     "nvk_decode_metadata": (ctypes.c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i32, _c_i32, _c_i32, _c_i32,
                                            _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr]),
+    "nvk_decode_graph_refresh": (ctypes.c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i32,
+                                                _c_i32, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64,
+                                                _c_i32, _c_ptr]),
     "nvk_uniform_cu_seqlens": (ctypes.c_int, [_c_ptr, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr]),
     "nvk_sample_workspace_size": (ctypes.c_size_t, [_c_i32, _c_i32]),
     "nvk_sample": (ctypes.c_int, [_c_ptr, _c_i64, _c_i32, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_i64,

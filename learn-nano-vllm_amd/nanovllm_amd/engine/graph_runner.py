@@ -25,6 +25,7 @@ from typing import Callable
 
 import torch
 
+from nanovllm_amd import _lib
 from nanovllm_amd.utils.context import get_context, reset_context, set_context
 
 
@@ -98,13 +99,25 @@ class DecodeGraphRunner:
             raise ValueError(f"batch {bs} above the largest captured bucket {self.max_bs}")
         context = get_context()
         graph = self.graphs[self.bucket(bs)]
-        self.positions[:bs] = positions
         for name, value in inputs.items():
             self.inputs[name][:bs] = value
-        self.slot_mapping.fill_(-1)
-        self.slot_mapping[:bs] = context.slot_mapping
-        self.context_lens.zero_()
-        self.context_lens[:bs] = context.context_lens
-        self.block_tables[:bs, :context.block_tables.size(1)] = context.block_tables
+        # run_model's refresh (slots -1 and contexts 0 past the live batch, the
+        # live block-table rectangle copied) in one kernel
+        pos = positions.to(torch.int64).contiguous()
+        slots = context.slot_mapping.to(torch.int32).contiguous()
+        lens = context.context_lens.to(torch.int32).contiguous()
+        bt = context.block_tables.to(torch.int32)
+        if bt.dim() != 2 or bt.size(0) != bs or bt.size(1) > self.block_tables.size(1):
+            raise ValueError(f"block_tables {tuple(bt.shape)} for batch {bs} and a static "
+                             f"width of {self.block_tables.size(1)}")
+        if bt.stride(1) != 1:
+            bt = bt.contiguous()
+        if slots.numel() != bs or lens.numel() != bs:
+            raise ValueError("slot_mapping and context_lens need one entry per sequence")
+        _lib.check(_lib.load().nvk_decode_graph_refresh(
+            pos.data_ptr(), slots.data_ptr(), lens.data_ptr(), bt.data_ptr(), bt.stride(0), bs,
+            bt.size(1), self.positions.data_ptr(), self.slot_mapping.data_ptr(),
+            self.context_lens.data_ptr(), self.block_tables.data_ptr(), self.block_tables.stride(0),
+            self.max_bs, _lib.stream_ptr(self.positions.device)))
         graph.replay()
         return self.outputs[:bs]

@@ -147,3 +147,55 @@ def test_large_buckets_replay_live_batches_below_their_bucket():
             ref = orc.paged_attention(q_ref, after[0, i], after[1, i], np.arange(live + 1), lens,
                                       D ** -0.5, block_tables=bt, block_size=BS)
             assert_attn_close(out[:, i].reshape(live, HQ, D), ref, f"replay {rep} layer {i}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bs,width", [(3, 5), (8, 7), (0, 5), (1, 1)])
+def test_graph_refresh_kernel_equals_run_model_copies(bs, width):
+    """nvk_decode_graph_refresh against run_model's tensor copies
+    (model_runner.py:200-211) on static buffers holding stale values: slots -1
+    and contexts 0 past the live batch, positions and block-table cells outside
+    the live rectangle untouched; the source table is a strided view."""
+    from nanovllm_amd import _lib
+    say(f"graph refresh kernel bs={bs} width={width}")
+    dev = torch.device("cuda:0")
+    rows, cols = 8, 7
+    g = torch.Generator().manual_seed(bs * 10 + width)
+    stale = lambda *shape, dt: torch.randint(-50, 50, shape, generator=g, dtype=dt).to(dev)
+    pos0, slot0 = stale(rows, dt=torch.int64), stale(rows, dt=torch.int32)
+    ctx0, bt0 = stale(rows, dt=torch.int32), stale(rows, cols, dt=torch.int32)
+    src_pos = torch.randint(0, 4096, (bs,), generator=g, dtype=torch.int64).to(dev)
+    src_slot = torch.randint(-1, 9000, (bs,), generator=g, dtype=torch.int32).to(dev)
+    src_ctx = torch.randint(0, 4096, (bs,), generator=g, dtype=torch.int32).to(dev)
+    src_bt = torch.randint(-1, 300, (bs, width + 2), generator=g, dtype=torch.int32).to(dev)[:, :width]
+    # reference: the copies of run_model
+    pos_r, slot_r, ctx_r, bt_r = pos0.clone(), slot0.clone(), ctx0.clone(), bt0.clone()
+    pos_r[:bs] = src_pos
+    slot_r.fill_(-1)
+    slot_r[:bs] = src_slot
+    ctx_r.zero_()
+    ctx_r[:bs] = src_ctx
+    bt_r[:bs, :width] = src_bt
+    pos, slot, ctx, bt = pos0.clone(), slot0.clone(), ctx0.clone(), bt0.clone()
+    lib = _lib.load()
+    rc = lib.nvk_decode_graph_refresh(src_pos.data_ptr(), src_slot.data_ptr(), src_ctx.data_ptr(),
+                                      src_bt.data_ptr(), src_bt.stride(0), bs, width,
+                                      pos.data_ptr(), slot.data_ptr(), ctx.data_ptr(),
+                                      bt.data_ptr(), bt.stride(0), rows,
+                                      torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    for got, ref, what in ((pos, pos_r, "positions"), (slot, slot_r, "slot_mapping"),
+                           (ctx, ctx_r, "context_lens"), (bt, bt_r, "block_tables")):
+        assert torch.equal(got, ref), what
+    # a batch above the static rows and a table wider than its stride are refused
+    assert lib.nvk_decode_graph_refresh(src_pos.data_ptr(), src_slot.data_ptr(),
+                                        src_ctx.data_ptr(), src_bt.data_ptr(), src_bt.stride(0),
+                                        rows + 1, width, pos.data_ptr(), slot.data_ptr(),
+                                        ctx.data_ptr(), bt.data_ptr(), bt.stride(0), rows,
+                                        torch.cuda.current_stream().cuda_stream) != 0
+    assert lib.nvk_decode_graph_refresh(src_pos.data_ptr(), src_slot.data_ptr(),
+                                        src_ctx.data_ptr(), src_bt.data_ptr(), src_bt.stride(0),
+                                        max(bs, 1), cols + 1, pos.data_ptr(), slot.data_ptr(),
+                                        ctx.data_ptr(), bt.data_ptr(), bt.stride(0), rows,
+                                        torch.cuda.current_stream().cuda_stream) != 0
