@@ -351,7 +351,7 @@ def mixed_leg(torch, dev, args, cpu_jobs, layers=28):
     def step():
         # the layers share the step's metadata: the prefill tiles are ranked once
         order = prefill_tile_order(t["cu_seqlens_q"], t["cu_seqlens_k"], meta["max_seqlen_q"],
-                                   pools[0][0], block_table=t["prefill_block_tables"],
+                                   pools[0][0], 16, block_table=t["prefill_block_tables"],
                                    max_seqlen_k=meta["max_seqlen_k"])
         main = torch.cuda.current_stream()
         for kc, vc in pools:

@@ -161,8 +161,15 @@ size_t nvk_paged_decode_workspace_size(int32_t batch, int32_t num_q_heads,
  * scratch: two calls that overlap on one GPU (different streams, or two host
  * threads) race and give undefined results; calls ordered on one stream are
  * safe.  Nothing in the scratch needs clearing between calls.
+ *
+ * nvk_paged_decode_noalloc_init: looks up the current device's scratch now
+ * (hipGetSymbolAddress) instead of at that device's first call.  Call it once
+ * per device, with the device current, before capturing
+ * nvk_paged_decode_noalloc into a graph, so that nothing but the kernel
+ * launches happens under capture.  Returns 0 or a hipError_t.
  */
 #define NVK_NOALLOC_SCRATCH_BYTES (20u << 20)
+int nvk_paged_decode_noalloc_init(void);
 int nvk_paged_decode_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                              const void* k_cache, const void* v_cache,
                              const int32_t* block_tables, int64_t bt_stride,
@@ -251,13 +258,19 @@ size_t nvk_varlen_prefill_workspace_size(int32_t batch, int32_t max_seqlen_q,
  *   use (min(max_seqlen_k, max_blocks*block_size) paged, min(max_seqlen_k,
  *   total_k) dense); block_size: the page size, 0 for dense keys.
  * nvk_prefill_tile_order: writes that order (one kernel; nothing when the
- *   size is 0).  order: device int32, 16-byte aligned, order_bytes >= size.
+ *   size is 0): a permutation of the (sequence, query tile) pairs followed by
+ *   a tag of the batch and the tile count.  order: device int32, 16-byte
+ *   aligned, order_bytes >= size.
  * nvk_varlen_prefill_ordered: nvk_varlen_prefill with the order given; it
- *   launches no ranking kernel.  The order must come from
- *   nvk_prefill_tile_order with the same cu_seqlens_q / cu_seqlens_k, batch,
- *   max_seqlen_q, key bound and head counts (else the output is
- *   unspecified; no access goes out of bounds).  NULL = nvk_varlen_prefill.
- *   Outputs are bit-identical to nvk_varlen_prefill's.
+ *   launches no ranking kernel.  order_bytes: the bytes of the order buffer;
+ *   when the call would use an order and order_bytes is below
+ *   nvk_prefill_tile_order_size() of its sizes, it returns NVK_EWORKSPACE
+ *   and launches nothing.  The order should come from nvk_prefill_tile_order
+ *   with the same metadata; the output is the same for any order: an order
+ *   ranked for other lengths of the same batch and tile count only runs the
+ *   tiles in a slower order, and one whose tag names another batch or tile
+ *   count is ignored (the tiles then run in grid order).  NULL =
+ *   nvk_varlen_prefill.  Outputs are bit-identical to nvk_varlen_prefill's.
  */
 size_t nvk_prefill_tile_order_size(int32_t batch, int32_t max_seqlen_q, int32_t max_keys,
                                    int32_t num_q_heads, int32_t num_kv_heads, int32_t block_size);
@@ -278,7 +291,7 @@ int nvk_varlen_prefill_ordered(const void* q, int64_t q_stride_tok, int64_t q_st
                                float scale,
                                void* out, int64_t out_stride_tok, int64_t out_stride_head,
                                void* workspace, size_t workspace_bytes, const int32_t* order,
-                               int32_t dtype, void* stream);
+                               size_t order_bytes, int32_t dtype, void* stream);
 
 /*
  * Fused attention prologue: q/k RMSNorm + rotary embedding + KV-store.

@@ -865,18 +865,12 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices];
 
-// Device address of this GPU's scratch, looked up once per device with that
-// device current (the device `stream` belongs to must be the current one).
-int scratch_for_stream(hipStream_t stream, void** ptr) {
+// Device address of the current device's scratch, looked up once per device
+// with that device current.
+int scratch_of_current_device(int* dev_out, void** ptr) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;
-  if (stream != nullptr) {
-    int sdev = -1;
-    e = hipStreamGetDevice(stream, &sdev);
-    if (e != hipSuccess) return (int)e;
-    if (sdev != dev) return NVK_EINVAL;
-  }
   if (dev < 0 || dev >= kMaxDevices) return NVK_EUNSUPPORTED;
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch_ptr[dev] == nullptr) {
@@ -886,7 +880,22 @@ int scratch_for_stream(hipStream_t stream, void** ptr) {
     if (p == nullptr || (uintptr_t)p % 256) return NVK_EALIGN;
     g_scratch_ptr[dev] = p;
   }
+  *dev_out = dev;
   *ptr = g_scratch_ptr[dev];
+  return NVK_OK;
+}
+
+// The scratch of the device `stream` belongs to, which must be the current one.
+int scratch_for_stream(hipStream_t stream, void** ptr) {
+  int dev = -1;
+  const int st = scratch_of_current_device(&dev, ptr);
+  if (st != NVK_OK) return st;
+  if (stream != nullptr) {
+    int sdev = -1;
+    const hipError_t e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return (int)e;
+    if (sdev != dev) return NVK_EINVAL;
+  }
   return NVK_OK;
 }
 
@@ -946,6 +955,12 @@ extern "C" int nvk_paged_decode_noalloc(const void* q, int64_t q_stride_tok,
   // Every descriptor and record the kernels read is written earlier in the
   // same call, so the scratch needs no clearing between calls.
   return decode_run(a, head_dim, ws, s);
+}
+
+extern "C" int nvk_paged_decode_noalloc_init(void) {
+  int dev = -1;
+  void* p = nullptr;
+  return scratch_of_current_device(&dev, &p);
 }
 
 extern "C" int nvk_paged_decode_prologue(

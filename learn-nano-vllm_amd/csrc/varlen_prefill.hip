@@ -108,6 +108,10 @@ constexpr int64_t kOrderMaxPairs = 1 << 22;
 // Below two rounds of the workgroup slots (256 CUs x 2) every tile starts at
 // once and the order cannot shorten the step: no extra kernel then.
 constexpr int64_t kOrderMinWgs = 1024;
+// Tag stored after the last pair of an order: batch < 2^13, n_qtiles < 2^16.
+__host__ __device__ __forceinline__ int32_t order_tag(int batch, int n_qtiles) {
+  return (int32_t)(0xA0000000u | ((uint32_t)batch << 16) | (uint32_t)n_qtiles);
+}
 static bool use_order(int batch, int64_t pairs, int num_kv_heads) {
   return batch > 1 && batch <= kOrderMaxBatch && pairs <= kOrderMaxPairs &&
          pairs * num_kv_heads > kOrderMinWgs;
@@ -178,8 +182,13 @@ __global__ __launch_bounds__(kOrderThreads) void prefill_tile_order_kernel(
   for (int i = 0; i < kPer; ++i) hist[kPer * tid + i] = start[i];  // cursors
   __syncthreads();
   for (int p = tid; p < P; p += kOrderThreads) order[atomicAdd(&hist[cost(p)], 1)] = p;
+  if (tid == 0) order[P] = order_tag(batch, n_qtiles);
 }
-static size_t order_bytes(int64_t pairs) { return (size_t)(pairs * 4 + 255) / 256 * 256; }
+// An order is the pairs [0, batch * n_qtiles) in some permutation, followed by
+// the tag of (batch, n_qtiles).  Any permutation of the same pairs gives the
+// same output, so an order ranked for other lengths but the same batch and
+// tile count is still correct; one whose tag differs is ignored (grid order).
+static size_t order_bytes(int64_t pairs) { return (size_t)((pairs + 1) * 4 + 255) / 256 * 256; }
 
 // Key range of one (sequence, query tile): shared by the attention and the
 // combine kernels.
@@ -281,7 +290,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     const int pairs = a.batch * a.n_qtiles;
     const int rank = blockIdx.y + a.batch * blockIdx.z;
     int p = ((const_i32*)a.order)[rank];
-    p = (unsigned)p < (unsigned)pairs ? p : rank;  // a damaged order stays in bounds
+    const int32_t tag = ((const_i32*)a.order)[pairs];
+    // an order of other sizes (tag) or a damaged one stays in bounds: grid order
+    p = (unsigned)p < (unsigned)pairs && tag == order_tag(a.batch, a.n_qtiles) ? p : rank;
     z = p / a.batch;
     s = p - z * a.batch;
   }
@@ -1037,7 +1048,8 @@ int varlen_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_he
                         int32_t num_blocks, int32_t num_q_heads, int32_t num_kv_heads,
                         int32_t head_dim, float scale, void* out, int64_t out_stride_tok,
                         int64_t out_stride_head, void* workspace, size_t workspace_bytes,
-                        int32_t dtype, void* stream, const int32_t* given_order) {
+                        int32_t dtype, void* stream, const int32_t* given_order,
+                        size_t given_order_bytes) {
   if (batch < 0 || max_seqlen_q < 0 || max_seqlen_k < 0 || num_q_heads <= 0 ||
       num_kv_heads <= 0 || total_q < 0 || total_k < 0)
     return NVK_EINVAL;
@@ -1147,6 +1159,8 @@ int varlen_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   const int64_t pairs = (int64_t)batch * sp.n_qtiles;
   if (sp.n_splits == 1 && use_order(batch, pairs, num_kv_heads)) {
     if (given_order) {
+      if (given_order_bytes < order_bytes(pairs)) return NVK_EWORKSPACE;
+      if ((uintptr_t)given_order % 4) return NVK_EALIGN;
       a.order = given_order;  // ranked once for every layer of the step
     } else if (workspace && workspace_bytes >= order_bytes(pairs)) {
       int32_t* order = static_cast<int32_t*>(workspace);
@@ -1179,7 +1193,7 @@ extern "C" int nvk_varlen_prefill(const void* q, int64_t q_stride_tok, int64_t q
                              batch, max_seqlen_q, max_seqlen_k, block_tables, bt_stride,
                              max_blocks, block_size, num_blocks, num_q_heads, num_kv_heads,
                              head_dim, scale, out, out_stride_tok, out_stride_head, workspace,
-                             workspace_bytes, dtype, stream, nullptr);
+                             workspace_bytes, dtype, stream, nullptr, 0);
 }
 
 extern "C" int nvk_varlen_prefill_ordered(
@@ -1190,13 +1204,13 @@ extern "C" int nvk_varlen_prefill_ordered(
     int32_t max_blocks, int32_t block_size, int32_t num_blocks, int32_t num_q_heads,
     int32_t num_kv_heads, int32_t head_dim, float scale, void* out, int64_t out_stride_tok,
     int64_t out_stride_head, void* workspace, size_t workspace_bytes, const int32_t* order,
-    int32_t dtype, void* stream) {
+    size_t order_bytes_, int32_t dtype, void* stream) {
   return varlen_prefill_impl(q, q_stride_tok, q_stride_head, total_q, k, v, k_stride_tok,
                              v_stride_tok, kv_stride_head, total_k, cu_seqlens_q, cu_seqlens_k,
                              batch, max_seqlen_q, max_seqlen_k, block_tables, bt_stride,
                              max_blocks, block_size, num_blocks, num_q_heads, num_kv_heads,
                              head_dim, scale, out, out_stride_tok, out_stride_head, workspace,
-                             workspace_bytes, dtype, stream, order);
+                             workspace_bytes, dtype, stream, order, order_bytes_);
 }
 
 extern "C" size_t nvk_prefill_tile_order_size(int32_t batch, int32_t max_seqlen_q,

@@ -42,6 +42,7 @@ SIGNATURES = {
                                                 _c_i64, _c_ptr, _c_i32, _c_i32, _c_i32, _c_i32,
                                                 _c_i32, _c_i32, _c_i32, ctypes.c_float, _c_ptr,
                                                 _c_i64, _c_i64, _c_i32, _c_ptr]),
+    "nvk_paged_decode_noalloc_init": (ctypes.c_int, []),
     "nvk_varlen_prefill": (ctypes.c_int, [_c_ptr, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i64,
                                           _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i32, _c_i32,
                                           _c_i32, _c_ptr, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
@@ -58,7 +59,8 @@ SIGNATURES = {
                                                   _c_i32, _c_i32, _c_i32, _c_ptr, _c_i64, _c_i32,
                                                   _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                                   ctypes.c_float, _c_ptr, _c_i64, _c_i64, _c_ptr,
-                                                  ctypes.c_size_t, _c_ptr, _c_i32, _c_ptr]),
+                                                  ctypes.c_size_t, _c_ptr, ctypes.c_size_t, _c_i32,
+                                                  _c_ptr]),
     "nvk_qk_norm_rope_store": (ctypes.c_int, [_c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr,
                                               ctypes.c_float, _c_ptr, _c_i64, _c_i64, _c_i32,
                                               _c_i32, _c_i32, _c_ptr, _c_i64, _c_i64, _c_ptr,
@@ -151,25 +153,36 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-# Workspaces of the attention wrappers, one per (device, stream), grown on
-# demand: calls on one stream run one after the other, so they can share it
-# (every kernel writes what it reads in the same call).  Buffers a larger one
-# replaces stay referenced, so a graph captured with them keeps valid memory.
+# Workspaces of the attention wrappers.
+#
+# Eager calls: one buffer per (device, stream), grown on demand.  Calls on one
+# stream run one after the other, so they can share it (every kernel writes
+# what it reads in the same call).  A buffer a larger one replaces is simply
+# dropped: torch's allocator returns it to the pool of the stream it was
+# allocated on, which only hands it out again to work ordered after the calls
+# that used it.
+#
+# Calls under graph capture: a fresh buffer per call, never cached.  It comes
+# from the graph's private memory pool, so it lives as long as the graph and
+# is never shared with eager calls, whatever stream handle torch later hands
+# out again (a replay may run beside eager work on another stream).  Graphs
+# that share one pool share its memory, as torch's own captured tensors do:
+# replay them one at a time, as the reference's bucketed decode graphs are.
 _workspaces: dict = {}
-_retired: list = []
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     """A uint8 device buffer of at least nbytes for the current stream of
     `device` (None for 0 bytes); torch's allocator hands out 512-byte aligned
-    blocks, and under graph capture the buffer comes from the graph's pool."""
+    blocks."""
     if nbytes <= 0:
         return None
+    with torch.cuda.device(device):
+        if torch.cuda.is_current_stream_capturing():
+            return torch.empty(nbytes, dtype=torch.uint8, device=device)
     key = (device.index, torch.cuda.current_stream(device).cuda_stream)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
-        if buf is not None:
-            _retired.append(buf)
         buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf

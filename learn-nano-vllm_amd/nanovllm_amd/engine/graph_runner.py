@@ -103,10 +103,15 @@ class DecodeGraphRunner:
             self.inputs[name][:bs] = value
         # run_model's refresh (slots -1 and contexts 0 past the live batch, the
         # live block-table rectangle copied) in one kernel
-        pos = positions.to(torch.int64).contiguous()
-        slots = context.slot_mapping.to(torch.int32).contiguous()
-        lens = context.context_lens.to(torch.int32).contiguous()
-        bt = context.block_tables.to(torch.int32)
+        # the refresh kernel reads these through raw pointers: they must live on
+        # the graph's GPU (the copies run_model makes would also accept host or
+        # other-device tensors; those are moved first)
+        dev = self.positions.device
+        pos = positions.to(device=dev, dtype=torch.int64).contiguous()
+        slots = context.slot_mapping.to(device=dev, dtype=torch.int32).contiguous()
+        lens = context.context_lens.to(device=dev, dtype=torch.int32).contiguous()
+        bt = context.block_tables.to(device=dev, dtype=torch.int32)
+        _lib.require_gpu(pos, slots, lens, bt)
         if bt.dim() != 2 or bt.size(0) != bs or bt.size(1) > self.block_tables.size(1):
             raise ValueError(f"block_tables {tuple(bt.shape)} for batch {bs} and a static "
                              f"width of {self.block_tables.size(1)}")

@@ -44,13 +44,14 @@ def _key_bound(k, block_table, max_seqlen_k):
     return min(int(max_seqlen_k), bound) if max_seqlen_k else bound
 
 
-def prefill_tile_order(cu_seqlens_q, cu_seqlens_k, max_seqlen_q, k, block_table=None,
-                       max_seqlen_k=None, num_q_heads=16):
+def prefill_tile_order(cu_seqlens_q, cu_seqlens_k, max_seqlen_q, k, num_q_heads,
+                       block_table=None, max_seqlen_k=None):
     """The longest-first order of a prefill's query tiles, for every layer of a
     step (they share cu_seqlens): pass it as ``order`` to varlen_prefill to
     skip the per-call ranking kernel.  k: the layer's keys or cache (only its
-    shape is read).  Returns an int32 device tensor, or None when the prefill
-    runs in grid order anyway."""
+    shape is read); num_q_heads: the q heads the prefill calls will have.
+    Returns an int32 device tensor, or None when the prefill runs in grid
+    order anyway."""
     dev = _lib.require_gpu(cu_seqlens_q, cu_seqlens_k)
     cu_q, cu_k = _int32(cu_seqlens_q), _int32(cu_seqlens_k)
     batch = cu_q.numel() - 1
@@ -120,8 +121,18 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_sc
     msk = min(int(max_seqlen_k), key_bound) if max_seqlen_k else key_bound
     ws_bytes = lib.nvk_varlen_prefill_workspace_size(batch, int(max_seqlen_q), msk, hq, hkv, d)
     ws = _lib.workspace(dev, ws_bytes)
-    if order is not None and (order.dtype != torch.int32 or not order.is_cuda):
-        raise _lib.NvkError("order must be the int32 device tensor prefill_tile_order returns")
+    order_bytes = 0
+    if order is not None:
+        if order.dtype != torch.int32 or order.device != dev or not order.is_contiguous():
+            raise _lib.NvkError("order must be the int32 device tensor prefill_tile_order returns")
+        order_bytes = order.numel() * 4
+        need = lib.nvk_prefill_tile_order_size(batch, int(max_seqlen_q), msk, hq, hkv,
+                                               block_size if bt is not None else 0)
+        if need == 0:
+            order = None          # this call runs its tiles in grid order
+        elif order_bytes < need:
+            raise _lib.NvkError(f"order holds {order_bytes} bytes; a prefill of these sizes "
+                                f"needs {need} (rank it with this call's sizes and head counts)")
     with torch.cuda.device(dev):
         code = lib.nvk_varlen_prefill_ordered(
             q.data_ptr(), q.stride(0), q.stride(1), tq,
@@ -130,7 +141,7 @@ def varlen_prefill(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, softmax_sc
             _lib.ptr(bt), bt_stride, max_blocks, block_size, num_blocks,
             hq, hkv, d, scale,
             out.data_ptr(), out.stride(0), out.stride(1),
-            _lib.ptr(ws), ws_bytes, _lib.ptr(order),
+            _lib.ptr(ws), ws_bytes, _lib.ptr(order), order_bytes,
             dtype, _lib.stream_ptr(dev))
     _lib.check(code)
     return out

@@ -53,8 +53,8 @@ def test_decode_context_ladder_and_group_sizes(hq, hkv):
 def test_decode_groups_cut_into_many_parts():
     """Two sequences over 1500 and 3000 keys: the stream-K split cuts each
     (sequence, kv head) group into ~24 and ~47 wave parts; the grid has more
-    than 32 waves per group, so the combine folds them in four interleaved
-    slices merged through LDS."""
+    than 32 waves per group, so the combine folds them in sixteen interleaved
+    slices (one per wave of a 1024-thread workgroup) merged through LDS."""
     case = decode_case(seed=11, ctx=[1500, 3000], pool_blocks=24)
     _check(case, "decode groups of 24 and 47 parts")
 

@@ -93,11 +93,14 @@ def test_order_ranked_once_serves_every_layer():
                        for _ in range(2)]
     dcu_q, dcu_k, dbt = cu_q.cuda(), cu_k.cuda(), bt.cuda()
     say("prefill order once per step: rank")
-    order = prefill_tile_order(dcu_q, dcu_k, max(lens_q), kc.cuda(), block_table=dbt,
+    order = prefill_tile_order(dcu_q, dcu_k, max(lens_q), kc.cuda(), 16, block_table=dbt,
                                max_seqlen_k=max(lens_k))
     assert order is not None
-    pairs = len(lens_q) * ((max(lens_q) + 63) // 64)
+    n_qtiles = (max(lens_q) + 63) // 64
+    pairs = len(lens_q) * n_qtiles
     assert sorted(order[:pairs].cpu().tolist()) == list(range(pairs))
+    # the tag after the pairs names the batch and the tile count
+    assert int(order[pairs]) == np.int32(np.uint32(0xA0000000 | (len(lens_q) << 16) | n_qtiles))
     for i, (q, kc, vc, bt_i, _, _) in enumerate(layers):
         assert torch.equal(bt_i, bt)
         dq, dkc, dvc = q.cuda(), kc.cuda(), vc.cuda()
@@ -112,3 +115,30 @@ def test_order_ranked_once_serves_every_layer():
     assert_attn_close(a, ref, "ordered prefill, last layer")
     # a launch that runs in grid order needs no order
     assert _lib.load().nvk_prefill_tile_order_size(3, 100, 1536, 16, 8, 256) == 0
+
+
+def test_order_of_other_sizes_is_rejected_or_ignored():
+    """An order buffer too small for the call is rejected before any launch;
+    an order ranked for another batch (its tag differs) is ignored and the
+    tiles run in grid order, with the output of an unordered call."""
+    from nanovllm_amd import _lib, varlen_prefill
+    from nanovllm_amd.flash_api import prefill_tile_order
+    rng = np.random.default_rng(78)
+    lens_q = [int(x) for x in rng.integers(64, 700, 48)]
+    lens_k = [q + int(c) for q, c in zip(lens_q, rng.integers(0, 900, len(lens_q)))]
+    q, kc, vc, bt, cu_q, cu_k = (x.cuda() for x in _paged_case(79, lens_q, lens_k))
+    args = (q, kc, vc, cu_q, cu_k, max(lens_q), 128 ** -0.5)
+    kw = dict(block_table=bt, max_seqlen_k=max(lens_k))
+    say("prefill order: a smaller batch's order")
+    small = prefill_tile_order(cu_q[:41], cu_k[:41], max(lens_q), kc, 16, block_table=bt[:40],
+                               max_seqlen_k=max(lens_k))
+    assert small is not None
+    with pytest.raises(_lib.NvkError, match="order holds"):
+        varlen_prefill(*args, order=small, **kw)
+    # a buffer large enough whose tag names another batch: ignored
+    big = torch.zeros(small.numel() + 4096, dtype=torch.int32, device="cuda")
+    big[:small.numel()] = small
+    ref = varlen_prefill(*args, **kw)
+    got = varlen_prefill(*args, order=big, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)

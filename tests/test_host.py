@@ -89,8 +89,10 @@ def test_error_codes_without_launching():
     assert lib.nvk_varlen_prefill_workspace_size(32, 6, 8192, 16, 8, 128) == max(split, short)
     # enough query tiles to fill the GPU and too many rows for the short path: the
     # longest-first tile order only, one int32 per (sequence, query tile) pair
-    # (32 x 1024/64), rounded up to 256 bytes
-    assert lib.nvk_varlen_prefill_workspace_size(32, 1024, 1536, 16, 8, 128) == 32 * 16 * 4
+    # (32 x 1024/64) and the order's tag, rounded up to 256 bytes
+    assert lib.nvk_varlen_prefill_workspace_size(32, 1024, 1536, 16, 8, 128) == \
+        (32 * 16 + 1) * 4 // 256 * 256 + 256
+    assert lib.nvk_prefill_tile_order_size(32, 1024, 1536, 16, 8, 256) == 2304
     # a grid of one round of workgroups (3 x 2 query tiles x 8 kv heads): no order
     assert lib.nvk_varlen_prefill_workspace_size(3, 100, 1536, 16, 8, 128) == 0
     # one sequence of 6 queries over 512 keys: no split; the short-query kernels'

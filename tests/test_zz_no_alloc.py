@@ -3,8 +3,11 @@ its workspace is a static device array inside the library) called through
 the C ABI, against nvk_paged_decode with a torch-allocated workspace: the
 same kernels, so the outputs must be bit-identical, on calls in a row whose
 sizes shrink (the scratch keeps the previous call's contents) and against
-the oracle within 2e-2 abs / 1e-2 rel.  Sizes beyond the scratch are
-rejected before anything is launched."""
+the oracle within 2e-2 abs / 1e-2 rel, and captured in a graph and
+replayed.  The rejection of sizes beyond the scratch is checked with fake
+pointers on a host without a GPU (tests/test_host.py): on a GPU a regression
+of that check would launch kernels that write past the scratch.  The GPU
+cases here only make calls whose sizes fit it."""
 import numpy as np
 import pytest
 import torch
@@ -14,8 +17,6 @@ from nanovllm_amd import _lib, paged_decode
 from nanovllm_amd.workloads import decode_case
 
 pytestmark = pytest.mark.gpu
-
-NVK_ESCRATCH = -5
 
 
 def _noalloc(lib, c, scale, out):
@@ -51,19 +52,36 @@ def test_noalloc_decode_equals_workspace_decode_on_shrinking_calls():
         assert_attn_close(out, ref, what)
 
 
-def test_noalloc_decode_rejects_sizes_beyond_its_scratch():
+def test_noalloc_decode_replays_under_graph_capture():
+    """Captured after nvk_paged_decode_noalloc_init (so only kernel launches
+    happen under capture), the no-allocation decode replays bit for bit like
+    nvk_paged_decode, replay after replay, with eager decodes of other sizes
+    (which reuse the same static scratch) run between the replays."""
     lib = _lib.load()
-    c = decode_case(seed=73, ctx=[5], pool_blocks=2).to("cuda")
-    out = torch.zeros(1, 16, 128, dtype=torch.bfloat16, device="cuda")
-    # 2048 sequences x 1024 kv heads x group 8: ~34 MB of workspace
-    rc = lib.nvk_paged_decode_noalloc(
-        c.q.data_ptr(), 128, 128, c.k_cache.data_ptr(), c.v_cache.data_ptr(),
-        c.block_tables.data_ptr(), 1, c.context_lens.data_ptr(), 2048, 8192, 1024, 128, 256, 1, 2,
-        0.088, out.data_ptr(), 128, 128, _lib.NVK_DTYPE_BF16,
-        torch.cuda.current_stream().cuda_stream)
-    assert rc == NVK_ESCRATCH
-    assert b"scratch" in lib.nvk_strerror(rc)
-    need = lib.nvk_paged_decode_workspace_size(2048, 8192, 1024, 128, 256, 1)
-    assert need > (20 << 20)
+    assert lib.nvk_paged_decode_noalloc_init() == 0
+    case = decode_case(seed=74, pool_blocks=600)
+    c = case.to("cuda")
+    other = decode_case(seed=75, ctx=[4000, 9, 2048], pool_blocks=40).to("cuda")
+    say("no-alloc decode under capture: reference")
+    ref = paged_decode(c.q, c.k_cache, c.v_cache, c.context_lens, c.block_tables, case.scale)
+    out = torch.zeros_like(ref)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):                    # warm-up off the capture
+        assert _noalloc(lib, c, case.scale, out) == 0
+    torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    assert out.eq(0).all(), "a rejected call must launch nothing"
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _noalloc(lib, c, case.scale, out)
+    assert rc == 0, lib.nvk_strerror(rc)
+    other_out = torch.empty_like(other.q)
+    for i in range(4):
+        say(f"no-alloc decode under capture: replay {i}")
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {i} differs from the workspace entry point"
+        # eager work between replays, on the same scratch
+        assert _noalloc(lib, other, case.scale, other_out) == 0
+        torch.cuda.synchronize()
