@@ -733,6 +733,50 @@ def copy_ceiling(torch, dev, nbytes, args):
     return round(2 * nbytes / ev / 1e9, 1)
 
 
+PROBE_LIB = os.path.join(ROOT, "learn-nano-vllm_amd", "bench_probe", "libnvk_probe.so")
+
+
+def stream_ceilings(torch, dev, args, store_bytes=None):
+    """GB/s that plain streaming kernels reach on this box (hand-written, 16 B
+    per lane, non-temporal; learn-nano-vllm_amd/bench_probe/stream_probe.hip):
+    read-only, write-only and copy over 512 MiB buffers, and a copy of the
+    store's own byte count, each under the >= 1 GiB rotation of the legs.
+    These are the rates a read + write kernel (the store, the prologue) and a
+    read kernel (the decode) can be held against, besides the 8 TB/s peak."""
+    import ctypes
+    lib = ctypes.CDLL(PROBE_LIB)
+    lib.nvk_probe_stream.restype = ctypes.c_int
+    lib.nvk_probe_stream.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_size_t, ctypes.c_void_p]
+
+    def call(mode, a, b, n):
+        rc = lib.nvk_probe_stream(mode, a.data_ptr() if a is not None else None, b.data_ptr(), n,
+                                  torch.cuda.current_stream(dev).cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"stream probe mode {mode}: error {rc}")
+
+    def rate(mode, nbytes, moved):
+        n = rotation(moved)
+        src = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(n)] \
+            if mode != 1 else [None] * n
+        dst = [torch.empty(nbytes if mode else 4096, dtype=torch.uint8, device=dev)
+               for _ in range(n)]
+        fns = [(lambda a=a, b=b: call(mode, a, b, nbytes)) for a, b in zip(src, dst)]
+        _, ev = time_graph(torch, fns, 20, 3, args.eager)
+        del src, dst, fns
+        return round(moved / ev / 1e9, 1)
+
+    big = 512 << 20
+    out = {"read_512mib_gbs": rate(0, big, big), "write_512mib_gbs": rate(1, big, big),
+           "copy_512mib_gbs": rate(2, big, 2 * big)}
+    if store_bytes:
+        half = (store_bytes // 2 + 15) // 16 * 16
+        out["copy_store_bytes_gbs"] = rate(2, half, 2 * half)
+    out["what"] = ("hand-written streaming kernels (16-byte non-temporal accesses, 4 per lane "
+                   "in flight): GB/s of bytes read, written, or read + written (copy)")
+    return out
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -817,6 +861,9 @@ def main():
         log("timing device copies of the same bytes and of 512 MiB")
         same = copy_ceiling(torch, dev, st_bytes // 2, args)
         big = copy_ceiling(torch, dev, 512 << 20, args)
+        log("timing streaming probes (read, write, copy)")
+        streams = stream_ceilings(torch, dev, args, st_bytes)
+        result["stream_ceiling"] = streams
         ach = st_bytes / ev_s / 1e9
         result["kv_store"] = dict(
             ms_per_step=wall_s * 1e3, bytes_per_step=st_bytes,
@@ -826,8 +873,12 @@ def main():
             copy_ceiling={"same_bytes_copy_gbs": same, "copy_512mib_gbs": big,
                           "frac_of_same_bytes_copy": round(ach / same, 4),
                           "frac_of_512mib_copy": round(ach / big, 4),
+                          "frac_of_copy_probe_512mib": round(ach / streams["copy_512mib_gbs"], 4),
+                          "frac_of_copy_probe_same_bytes":
+                              round(ach / streams["copy_store_bytes_gbs"], 4),
                           "what": "torch device-to-device copy reading and writing the store's "
-                                  "bytes (and 512 MiB), same rotation, GB/s of read + write"})
+                                  "bytes (and 512 MiB), same rotation, GB/s of read + write; "
+                                  "the probes' figures are in stream_ceiling"})
         if not args.no_cpu_baseline:
             def store_cpu():
                 from oracle import torch_cpu as tcpu
@@ -846,6 +897,10 @@ def main():
     # ------------------------------------------------------------------ prologue
     if "prologue" in legs:
         result["prologue"] = prologue_leg(torch, dev, args, cpu_jobs)
+        if "stream_ceiling" in result:   # a read + write stream, like a copy
+            r = result["prologue"]["roofline"]
+            r["frac_of_copy_probe"] = round(
+                r["achieved"] / result["stream_ceiling"]["copy_512mib_gbs"], 4)
 
     # ------------------------------------------------------------------ prefill
     if "prefill" in legs:
@@ -981,8 +1036,11 @@ def main():
                      "traffic": traffic_for("decode")},
         "cpu_baseline": cpu,
     }
+    if "stream_ceiling" in result:   # the decode is a read stream
+        line["roofline"]["frac_of_read_probe"] = round(
+            d["event_gbs"] / result["stream_ceiling"]["read_512mib_gbs"], 4)
     for k in ("kv_store", "prologue", "prefill", "spec_verify", "decode_graph", "step_metadata",
-              "sampler", "mixed_step"):
+              "sampler", "mixed_step", "stream_ceiling"):
         if k in result:
             line[k] = result[k]
     print(json.dumps(line), flush=True)

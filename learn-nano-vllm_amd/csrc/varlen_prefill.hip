@@ -558,15 +558,24 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       }
     }
   };
-  // Row max of a tile as a chain of 15 v_max3 steps (step 0 takes scores 0-2,
-  // step st > 0 scores 2st+1 and 2st+2) and a final max with score 31, so the
-  // steps can be spread over MFMAs; score i of the 32 is sc[i / 16][i % 16].
-  auto max_step = [&](const nvk_f32x16 (&sc)[2], float mx, int st) -> float {
+  // Row max of a tile (score i of the 32 is sc[i / 16][i % 16]) in four
+  // chains, chain c over scores 8c..8c+6 in three v_max3 steps, then a join
+  // with scores 7, 15, 23, 31.  The steps can be spread over MFMAs, and two
+  // chains advance side by side: a v_max3 (inline asm) that reads the result
+  // of the one just before it costs a wait state.
+  auto max_chain = [&](const nvk_f32x16 (&sc)[2], float x, int c, int st) -> float {
     auto v = [&](int i) { return sc[i >> 4][i & 15]; };
-    return st == 0 ? nvk_max3(v(0), v(1), v(2)) : nvk_max3(mx, v(2 * st + 1), v(2 * st + 2));
+    const int b = 8 * c;
+    return st == 0 ? nvk_max3(v(b), v(b + 1), v(b + 2))
+                   : nvk_max3(x, v(b + 2 * st + 1), v(b + 2 * st + 2));
   };
-  auto max_finish = [&](const nvk_f32x16 (&sc)[2], float mx) -> float {
-    return nvk_max_xor32(fmaxf(mx, sc[1][15])) * a.scale_log2;  // tile max, log2 units
+  auto max_join_a = [&](const nvk_f32x16 (&sc)[2], const float (&ch)[4], float (&t)[2]) {
+    t[0] = nvk_max3(ch[0], ch[1], sc[0][7]);
+    t[1] = nvk_max3(ch[2], ch[3], sc[0][15]);
+  };
+  auto max_join_b = [&](const nvk_f32x16 (&sc)[2], const float (&t)[2]) -> float {
+    const float u = nvk_max3(t[0], t[1], sc[1][7]);
+    return nvk_max_xor32(fmaxf(u, sc[1][15])) * a.scale_log2;  // tile max, log2 units
   };
   // Lazy rescale for a tile whose row max (log2 units) is mt; returns the
   // offset for exp2.
@@ -585,17 +594,33 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     }
     return m_ref == -INFINITY ? 0.f : m_ref;  // row masked so far: p = 0
   };
-  // Word e of P fragment p (keys 16p..16p+15 of the tile, in accumulator
-  // order): exp2(score * scale_log2 - moff) of two scores packed to bf16; the
-  // row sum accumulates the same rounded values that enter the PV product.
-  auto exp_word = [&](const nvk_f32x16 (&sc)[2], float moff, int p, int e) -> uint32_t {
+  // Word n = 4p + e of the tile's probabilities (word e of P fragment p: keys
+  // 16p..16p+15 of the tile, in accumulator order): exp2(score * scale_log2 -
+  // moff) of two scores packed to bf16; the row sum accumulates the same
+  // rounded values that enter the PV product.  A word is made in two halves,
+  // the exp2 pair (exp_start) and the packing (exp_finish), and the loop
+  // starts word n + 1 before it finishes word n: a packing that reads an
+  // exp2 result in the next instruction waits a cycle (an s_nop per word).
+  struct ExpPair {
+    float p0, p1;
+  };
+  auto exp_start = [&](const nvk_f32x16 (&sc)[2], float moff, int n) -> ExpPair {
+    const int p = n >> 2, e = n & 3;
     const int mb = p >> 1, i = 8 * (p & 1) + 2 * e;
-    const float p0 = nvk_fast_exp2(fmaf(sc[mb][i], a.scale_log2, -moff));
-    const float p1 = nvk_fast_exp2(fmaf(sc[mb][i + 1], a.scale_log2, -moff));
-    uint32_t w = E::pack2(p0, p1);
-    l_part[e & 1] = E::dot2(w, E::kOnes, l_part[e & 1]);  // the pair (1, 1)
+    ExpPair x;
+    x.p0 = nvk_fast_exp2(fmaf(sc[mb][i], a.scale_log2, -moff));
+    x.p1 = nvk_fast_exp2(fmaf(sc[mb][i + 1], a.scale_log2, -moff));
+    asm volatile("" : "+v"(x.p0), "+v"(x.p1));  // issued here
+    return x;
+  };
+  auto exp_finish = [&](ExpPair x, int n) -> uint32_t {
+    // packed no earlier than here (a fence, not an asm statement: the hazard
+    // check would take an asm writing p0 / p1 for a transcendental)
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t w = E::pack2(x.p0, x.p1);
+    l_part[n & 1] = E::dot2(w, E::kOnes, l_part[n & 1]);  // the pair (1, 1)
     // keep this word where it is placed among the MFMAs (no sinking to its use)
-    asm volatile("" : "+v"(w), "+v"(l_part[e & 1]));
+    asm volatile("" : "+v"(w), "+v"(l_part[n & 1]));
     return w;
   };
 
@@ -655,8 +680,15 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     vec8 vf[3];
     vf[0] = rd_v(0, 0);
     vf[1] = rd_v(1, 0);
+    // words 0-3 (fragment 0) before the first MFMA; word n lives in xp[n & 1]
+    // from its start to its finish
+    ExpPair xp[2];
+    xp[0] = exp_start(sc, moff, 0);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) pw[e] = exp_word(sc, moff, 0, e);
+    for (int n = 0; n < 4; ++n) {
+      xp[(n + 1) & 1] = exp_start(sc, moff, n + 1);
+      pw[n] = exp_finish(xp[n & 1], n);
+    }
     pf[0] = pack(pw);
     __builtin_amdgcn_sched_barrier(0);
     constexpr int kO = (kKeys / 16) * (HD / 32);
@@ -668,11 +700,12 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       const int j = v_load_at(idx);
       if (j >= 0) issue_load(plan_v, j, true);
     };
-    // O k-step 0 with fragment 1.
+    // O k-step 0 with fragment 1 (words 4-7; word 8 started).
 #pragma unroll
     for (int idx = 0; idx < 4; ++idx) {
       o_mfma(idx);
-      pw[idx] = exp_word(sc, moff, 1, idx);
+      pw[idx] = exp_finish(xp[idx & 1], 4 + idx);
+      xp[(5 + idx) & 1] = exp_start(sc, moff, 5 + idx);
       __builtin_amdgcn_sched_barrier(0);
     }
     pf[1] = pack(pw);
@@ -689,9 +722,11 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
         if (ks + 2 < HD / 16) kf[(ks + 2) % 3] = rd_k(ks + 2, mb);
         __builtin_amdgcn_sched_barrier(0);
         sc[mb] = E::mfma32x32x16(kf[ks % 3], qf[ks], sc[mb]);
-        if (mb == 0) {
-          if (ks < 4) pw[ks] = exp_word(sc, moff, 2, ks);
-          else pw3[ks - 4] = exp_word(sc, moff, 3, ks - 4);
+        if (mb == 0) {  // fragments 2-3: words 8-15
+          const uint32_t w = exp_finish(xp[ks & 1], 8 + ks);
+          if (ks < 4) pw[ks] = w;
+          else pw3[ks - 4] = w;
+          if (ks < 7) xp[(9 + ks) & 1] = exp_start(sc, moff, 9 + ks);
         }
         const int j = k_load_at(8 * mb + ks);
         if (j >= 0) issue_load(plan_k, j, false);
@@ -714,16 +749,23 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       }
     }
     mask_tile(sc, kt + 1);
-    // O k-steps 1-3 with the row max of S(kt+1) (15 max3 steps over 8 MFMAs).
-    float mx = 0.f;
+    // O k-steps 1-3 with the row max of S(kt+1): chains 0-1 (score block 0)
+    // beside MFMAs 4-6, chains 2-3 (block 1, just computed) beside 8-10, the
+    // join beside 11-12.
+    float ch[4] = {0.f, 0.f, 0.f, 0.f}, tj[2];
 #pragma unroll
     for (int idx = 4; idx < kO; ++idx) {
       o_mfma(idx);
-      if (idx < 12) {
-        mx = max_step(sc, mx, 2 * (idx - 4));
-        if (2 * (idx - 4) + 1 < 15) mx = max_step(sc, mx, 2 * (idx - 4) + 1);
+      if (idx >= 4 && idx < 7) {
+        ch[0] = max_chain(sc, ch[0], 0, idx - 4);
+        ch[1] = max_chain(sc, ch[1], 1, idx - 4);
       }
-      if (idx == 12) mt_next = max_finish(sc, mx);
+      if (idx >= 8 && idx < 11) {
+        ch[2] = max_chain(sc, ch[2], 2, idx - 8);
+        ch[3] = max_chain(sc, ch[3], 3, idx - 8);
+      }
+      if (idx == 11) max_join_a(sc, ch, tj);
+      if (idx == 12) mt_next = max_join_b(sc, tj);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -774,10 +816,13 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     mask_tile(sc, tb);
     float mt;
     {
-      float mx = 0.f;
+      float ch[4] = {0.f, 0.f, 0.f, 0.f}, tj[2];
 #pragma unroll
-      for (int st = 0; st < 15; ++st) mx = max_step(sc, mx, st);
-      mt = max_finish(sc, mx);
+      for (int st = 0; st < 3; ++st)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ch[c] = max_chain(sc, ch[c], c, st);
+      max_join_a(sc, ch, tj);
+      mt = max_join_b(sc, tj);
     }
     auto step = [&](auto par, int kt) {
       constexpr int P = decltype(par)::value;
