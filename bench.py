@@ -524,23 +524,38 @@ def decode_graph_leg(torch, dev, args, layers=28):
     from nanovllm_amd.utils.context import reset_context, set_context
     from nanovllm_amd.workloads import attention_bytes, decode_case, decode_stack, prologue_bytes
 
+    from nanovllm_amd.layers.prologue import attention_with_prologue
+
     dc = decode_case()
     b, nb, w = 64, dc.k_cache.shape[0], dc.block_tables.shape[1]
     log(f"building {layers}-layer decode stack (30 GB of KV cache) and capturing buckets")
-    stack, _, kv_cache, step = decode_stack(layers, nb, dev)
+    stack, rope, kv_cache, _ = decode_stack(layers, nb, dev)
+
+    def step(positions, qkv):
+        # every layer's kernels run; the step returns the last layer's output,
+        # as a model step returns its last hidden state (run_model copies that
+        # one tensor into the graph's output buffer, model_runner.py:245)
+        out = None
+        for i, (attn, qn, kn) in enumerate(stack):
+            out = attention_with_prologue(attn, positions, qkv[:, i], qn, kn, rope)
+        return out.reshape(positions.numel(), 16 * 128)
+
     r = 16 + 2 * 8
     runner = DecodeGraphRunner(step, b, w, inputs={"qkv": ((layers, r * 128), torch.bfloat16)},
-                               output=((layers, 16 * 128), torch.bfloat16), device=dev)
+                               output=((16 * 128,), torch.bfloat16), device=dev)
     gen = torch.Generator(device=dev).manual_seed(7)
     qkv = (torch.randn(b, layers, r * 128, generator=gen, device=dev) * 2.0).to(torch.bfloat16)
     lens = dc.context_lens.to(dev)
     slots = torch.tensor([int(dc.block_tables[i, (n - 1) // 256]) * 256 + (n - 1) % 256
                           for i, n in enumerate(dc.lens)], dtype=torch.int32, device=dev)
     pos = (lens - 1).to(torch.int64)
-    steps, warm = min(args.steps, 20), min(args.warmup, 3)
+    steps = min(args.steps, 10)
 
     def timed(n):
-        """(graph replay, eager) seconds per step for the first n sequences."""
+        """(graph replay, eager) seconds per step for the first n sequences:
+        medians of TIMED_REPS + 2 rounds, each round timing `steps` replays
+        (run(): refresh + replay) and `steps` eager steps by HIP events, one
+        after the other, after a time-based warm-up of both."""
         set_context(False, slot_mapping=slots[:n], context_lens=lens[:n],
                     block_tables=dc.block_tables[:n].to(dev))
         # In the model the qkv rows are made inside the graph (the projection
@@ -548,18 +563,27 @@ def decode_graph_leg(torch, dev, args, layers=28):
         # metadata, as run_model does (model_runner.py:200-211).  So the rows
         # are put in the graph's input buffer once, not copied every step.
         runner.inputs["qkv"][:n] = qkv[:n]
+        fns = (lambda: runner.run(pos[:n]), lambda: step(pos[:n], qkv[:n]))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        e1.record()
         try:
-            out = []
-            for fn in (lambda: runner.run(pos[:n]), lambda: step(pos[:n], qkv[:n])):
-                for _ in range(warm):
+            t_warm = time.perf_counter()
+            while time.perf_counter() - t_warm < MIN_WARM_S:
+                for fn in fns:
                     fn()
                 torch.cuda.synchronize()
-                t0 = time.perf_counter()
-                for _ in range(steps):
-                    fn()
-                torch.cuda.synchronize()
-                out.append((time.perf_counter() - t0) / steps)
-            return out
+            out = ([], [])
+            for _ in range(TIMED_REPS + 2):
+                for fn, ts in zip(fns, out):
+                    torch.cuda.synchronize()
+                    e0.record()
+                    for _ in range(steps):
+                        fn()
+                    e1.record()
+                    torch.cuda.synchronize()
+                    ts.append(e0.elapsed_time(e1) / 1e3 / steps)
+            return [statistics.median(ts) for ts in out]
         finally:
             reset_context()
 
@@ -577,7 +601,9 @@ def decode_graph_leg(torch, dev, args, layers=28):
                 layers=layers, bytes_per_step=total,
                 workload=f"{layers} layers x (fused q/k norm + RoPE + store of 64 new tokens, "
                          "paged decode B=64 over U{100..2048}), bucket 64 of "
-                         "[1, 2, 4, 8, 16, 32, 48, 64], graph replays",
+                         "[1, 2, 4, 8, 16, 32, 48, 64], graph replays (refresh + replay) "
+                         "against the same step launched eagerly, HIP-event medians of "
+                         "interleaved rounds",
                 roofline={"bound": "hbm", "achieved": round(total / t_graph / 1e9, 2),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(total / t_graph / 1e9 / HBM_PEAK_GBS, 4)})

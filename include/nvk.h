@@ -303,11 +303,12 @@ int nvk_varlen_prefill_ordered(const void* q, int64_t q_stride_tok, int64_t q_st
  *
  * For every token t in [0, n_tokens) and head row of qkv[t] =
  * [q (num_q_heads rows) | k (num_kv_heads rows) | v (num_kv_heads rows)],
- * each row head_dim bf16 contiguous, token row stride qkv_row_stride:
- *     q, k rows: x = float(row); x *= rsqrt(mean(x^2) + eps); x = bf16(x);
- *                x = bf16(x * weight)            (q_norm_weight / k_norm_weight)
+ * each row head_dim elements of type T (bf16 or f16) contiguous, token row
+ * stride qkv_row_stride:
+ *     q, k rows: x = float(row); x *= rsqrt(mean(x^2) + eps); x = T(x);
+ *                x = T(x * weight)               (q_norm_weight / k_norm_weight, T)
  *                rotated by cos_sin_cache[positions[t]] (halves cos | sin,
- *                rotate-half convention) and rounded to bf16
+ *                rotate-half convention) and rounded to T
  *     q_out[t, h]                      = rotated q row h
  *     k_out[t, h]                      = rotated k row h        (k_out may be NULL)
  *     k_cache row slot_mapping[t], h   = rotated k row h        (slot -1 skipped)
@@ -320,9 +321,11 @@ int nvk_varlen_prefill_ordered(const void* q, int64_t q_stride_tok, int64_t q_st
  * reference skips the store while the caches are empty, attention.py:62);
  * otherwise caches as in nvk_kv_store with cache_slots = num_blocks*block_size
  * and slots outside [0, cache_slots) skipped.  positions: int64 [n_tokens].
- * dtype: NVK_DTYPE_BF16.  head_dim: 128.  Pointers 16-byte aligned, strides
- * multiples of 8 elements (cos_sin_row_stride of 4), n_tokens < 2^31.  One
- * kernel (one workgroup per token), nothing allocated.
+ * dtype (T of qkv, the weights, q_out, k_out and the caches): NVK_DTYPE_BF16
+ * or NVK_DTYPE_F16 (the model's dtype, model_runner.py:29).  head_dim: 128.
+ * Pointers 16-byte aligned, strides multiples of 8 elements
+ * (cos_sin_row_stride of 4), n_tokens < 2^31.  One kernel (one workgroup per
+ * token), nothing allocated.
  */
 int nvk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, int64_t n_tokens,
                            const int64_t* positions, const void* q_norm_weight,
@@ -350,7 +353,9 @@ int nvk_qk_norm_rope_store(const void* qkv, int64_t qkv_row_stride, int64_t n_to
  * lengths, workspace (nvk_paged_decode_workspace_size) and empty contexts as
  * in nvk_paged_decode; norm weights, eps, cos_sin_cache and positions as in
  * nvk_qk_norm_rope_store.  The result equals the two calls' bit for bit.
- * head_dim: 128.  Two kernels are enqueued (decode with prologue, combine).
+ * dtype: NVK_DTYPE_BF16 or NVK_DTYPE_F16 (qkv, weights, caches and out
+ * alike).  head_dim: 128.  Two kernels are enqueued (decode with prologue,
+ * combine).
  */
 int nvk_paged_decode_prologue(
     const void* qkv, int64_t qkv_row_stride, const int64_t* positions, const void* q_norm_weight,

@@ -61,6 +61,10 @@ struct NvkElt<false> {  // bf16
   static NVK_DEVICE uint32_t pack2(float lo, float hi) { return nvk_pack_bf16x2(lo, hi); }
   static NVK_DEVICE float dot2(uint32_t a, uint32_t b, float c) { return nvk_dot2_bf16(a, b, c); }
   static NVK_DEVICE uint16_t one(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+  // the low / high element of a packed pair, widened; x rounded to the type
+  static NVK_DEVICE float lo(uint32_t w) { return nvk_bf16lo_to_f32(w); }
+  static NVK_DEVICE float hi(uint32_t w) { return nvk_bf16hi_to_f32(w); }
+  static NVK_DEVICE float round(float x) { return nvk_bf16hi_to_f32((uint32_t)one(x) << 16); }
   static NVK_DEVICE nvk_f32x16 mfma32x32x16(vec8 a, vec8 b, nvk_f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
@@ -82,6 +86,13 @@ struct NvkElt<true> {  // f16
                                   __builtin_bit_cast(nvk_f16x2, b), c, false);
   }
   static NVK_DEVICE uint16_t one(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+  static NVK_DEVICE float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  static NVK_DEVICE float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  static NVK_DEVICE float round(float x) { return (float)(_Float16)x; }
   static NVK_DEVICE nvk_f32x16 mfma32x32x16(vec8 a, vec8 b, nvk_f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }

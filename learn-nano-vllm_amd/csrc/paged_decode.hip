@@ -298,7 +298,7 @@ __device__ __forceinline__ void fused_load(const DecodeArgs& a, int b, int64_t p
     in.kw = *reinterpret_cast<const nvk_u32x4*>(a.k_weight + 8 * r.j);
   }
 }
-template <int HD, int G>
+template <int HD, int G, bool F16>
 __device__ __forceinline__ void fused_apply(const DecodeArgs& a, const FusedIn<G>& in, int b,
                                             int kvh, int slot, bool need_q, bool need_new, int base,
                                             int ctx, int tpi, const LaneRole& r, nvk_u32x4* sq,
@@ -306,10 +306,11 @@ __device__ __forceinline__ void fused_apply(const DecodeArgs& a, const FusedIn<G
   if (need_q) {
 #pragma unroll
     for (int h = 0; h < G; ++h)
-      sq[h * nvk_qk::kLanesPerRow + r.j] = nvk_qk::norm_rope8_cs(in.q[h], in.qw, a.eps, in.cs, r.j);
+      sq[h * nvk_qk::kLanesPerRow + r.j] =
+          nvk_qk::norm_rope8_cs<F16>(in.q[h], in.qw, a.eps, in.cs, r.j);
   }
   if (need_new) {
-    const nvk_u32x4 kn = nvk_qk::norm_rope8_cs(in.k, in.kw, a.eps, in.cs, r.j);
+    const nvk_u32x4 kn = nvk_qk::norm_rope8_cs<F16>(in.k, in.kw, a.eps, in.cs, r.j);
     const int rel = ctx - 1 - base;
     const int i_new = rel / tpi, tt_new = rel % tpi;
 #pragma unroll
@@ -438,7 +439,6 @@ __device__ __forceinline__ void store_x8(uint16_t* p, const float* v, float scal
 
 template <int HD, int G, bool ALIGNED, bool FUSED, bool F16>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
-  static_assert(!(FUSED && F16), "the fused prologue is built for bf16");
   using CB = ChunkBuf<HD, G>;
   constexpr int RPI = 64 / CB::LPR;           // head rows per load instruction
   constexpr int REC_HEAD = G * (HD + 4);      // floats per head in a record
@@ -504,7 +504,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
       if (need_q || need_new) fused_load<HD, G>(a, cur.b, pos, kvh, need_q, need_new, role, in);
       load_chunk<HD, G, ALIGNED, FUSED>(a, cur, ctx, role, tpi, buf);
       if (need_q || need_new)
-        fused_apply<HD, G>(a, in, cur.b, kvh, slot, need_q, need_new, cur.k * a.tc, ctx, tpi, role, sq,
+        fused_apply<HD, G, F16>(a, in, cur.b, kvh, slot, need_q, need_new, cur.k * a.tc, ctx, tpi, role, sq,
                            buf);
 #pragma unroll
       for (int h = 0; h < G; ++h) {
@@ -976,7 +976,8 @@ extern "C" int nvk_paged_decode_prologue(
       num_blocks < 0 || cache_slots < 0 || !(eps >= 0.f))
     return NVK_EINVAL;
   if (!(scale > 0.f)) return NVK_EINVAL;
-  if (dtype != NVK_DTYPE_BF16 || head_dim != nvk_qk::kHD) return NVK_EUNSUPPORTED;
+  if ((dtype != NVK_DTYPE_BF16 && dtype != NVK_DTYPE_F16) || head_dim != nvk_qk::kHD)
+    return NVK_EUNSUPPORTED;
   if (num_q_heads % num_kv_heads) return NVK_EINVAL;
   const int G = num_q_heads / num_kv_heads;
   if (G != 1 && G != 2 && G != 4 && G != 8) return NVK_EUNSUPPORTED;
@@ -1042,5 +1043,8 @@ extern "C" int nvk_paged_decode_prologue(
   a.k_store = static_cast<uint16_t*>(k_cache);
   a.v_store = static_cast<uint16_t*>(v_cache);
   const bool aligned = (block_size % tc) == 0;
-  return dispatch_group<128, true>(a, G, aligned, reinterpret_cast<hipStream_t>(stream));
+  a.f16 = dtype == NVK_DTYPE_F16;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (a.f16) return dispatch_group<128, true, true>(a, G, aligned, s);
+  return dispatch_group<128, true>(a, G, aligned, s);
 }

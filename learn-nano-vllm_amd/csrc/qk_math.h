@@ -2,12 +2,14 @@
 // shared by the fused prologue kernel and the decode kernel that applies the
 // prologue itself, so that both produce the same bits.
 //
-// Semantics (nanovllm/layers/layernorm.py:16-26, rotary_embedding.py:6-14):
-//   x = row.float(); x *= rsqrt(mean(x^2) + eps); x = bf16(x) * weight (bf16)
+// Semantics (nanovllm/layers/layernorm.py:16-26, rotary_embedding.py:6-14),
+// with T the model's element type (bf16 or f16, model_runner.py:29):
+//   x = row.float(); x *= rsqrt(mean(x^2) + eps); x = T(x) * weight (T)
 //   x1, x2 = halves of x; cos, sin = halves of cos_sin_cache[pos]
-//   y1 = x1*cos - x2*sin ; y2 = x2*cos + x1*sin ; bf16(cat(y1, y2))
+//   y1 = x1*cos - x2*sin ; y2 = x2*cos + x1*sin ; T(cat(y1, y2))
 // Every f32 product and sum is rounded on its own (no fused multiply-add), as
-// the reference's separate tensor operations do.
+// the reference's separate tensor operations do; a product of two T values
+// is formed in f32 and rounded to T, as torch's elementwise kernels do.
 //
 // Lane mapping: a row group of 16 consecutive lanes owns the row, lane j
 // holds elements 8j .. 8j+7 (16 bytes).  The sum of squares is a 16-lane DPP
@@ -25,25 +27,24 @@ namespace nvk_qk {
 constexpr int kHD = 128;
 constexpr int kLanesPerRow = kHD / 8;  // 16
 
-__device__ __forceinline__ float bf16_round(float x) {
-  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) << 16);
-}
-
-// raw: this lane's 8 bf16 of the head row; wraw: its 8 bf16 of the norm
+// raw: this lane's 8 elements (T) of the head row; wraw: its 8 T of the norm
 // weight; cs: the lane's cos[8(j%8) .. +7] (cs[0..1]) and sin[8(j%8) .. +7]
-// (cs[2..3]) as f32.  Returns the lane's 8 rotated bf16, packed.
+// (cs[2..3]) as f32.  Returns the lane's 8 rotated T, packed.  F16: T = f16,
+// else bf16.
+template <bool F16>
 __device__ __forceinline__ nvk_u32x4 norm_rope8_cs(nvk_u32x4 raw, nvk_u32x4 wraw, float eps,
                                                    const nvk_u32x4 (&cs)[4], int j) {
 #pragma clang fp contract(off)
+  using E = NvkElt<F16>;
   float x[8];
   const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    x[2 * i] = nvk_bf16lo_to_f32(w4[i]);
-    x[2 * i + 1] = nvk_bf16hi_to_f32(w4[i]);
+    x[2 * i] = E::lo(w4[i]);
+    x[2 * i + 1] = E::hi(w4[i]);
   }
-  // RMSNorm: var = mean(x^2) over the row (f32), x * rsqrt(var + eps) -> bf16,
-  // then times the bf16 weight -> bf16.
+  // RMSNorm: var = mean(x^2) over the row (f32), x * rsqrt(var + eps) -> T,
+  // then times the T weight -> T.
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
@@ -52,9 +53,9 @@ __device__ __forceinline__ nvk_u32x4 norm_rope8_cs(nvk_u32x4 raw, nvk_u32x4 wraw
   const uint32_t ww[4] = {wraw.x, wraw.y, wraw.z, wraw.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float n0 = bf16_round(x[2 * i] * rstd), n1 = bf16_round(x[2 * i + 1] * rstd);
-    x[2 * i] = bf16_round(n0 * nvk_bf16lo_to_f32(ww[i]));
-    x[2 * i + 1] = bf16_round(n1 * nvk_bf16hi_to_f32(ww[i]));
+    const float n0 = E::round(x[2 * i] * rstd), n1 = E::round(x[2 * i + 1] * rstd);
+    x[2 * i] = E::round(n0 * E::lo(ww[i]));
+    x[2 * i + 1] = E::round(n1 * E::hi(ww[i]));
   }
   // Rotation: lanes 0-7 hold x1 (dims 0..63), lanes 8-15 x2 (dims 64..127).
   float cv[8], sv[8];
@@ -78,15 +79,16 @@ __device__ __forceinline__ nvk_u32x4 norm_rope8_cs(nvk_u32x4 raw, nvk_u32x4 wraw
     y[e] = first_half ? a0 - a1 : a0 + a1;  // x1*cos - x2*sin | x2*cos + x1*sin
   }
   nvk_u32x4 out;
-  out.x = nvk_pack_bf16x2(y[0], y[1]);
-  out.y = nvk_pack_bf16x2(y[2], y[3]);
-  out.z = nvk_pack_bf16x2(y[4], y[5]);
-  out.w = nvk_pack_bf16x2(y[6], y[7]);
+  out.x = E::pack2(y[0], y[1]);
+  out.y = E::pack2(y[2], y[3]);
+  out.z = E::pack2(y[4], y[5]);
+  out.w = E::pack2(y[6], y[7]);
   return out;
 }
 
 // The same with the cos/sin row read here: cs is the position's row (64 cos
 // then 64 sin, f32).
+template <bool F16>
 __device__ __forceinline__ nvk_u32x4 norm_rope8(nvk_u32x4 raw, nvk_u32x4 wraw, float eps,
                                                 const float* cs, int j) {
   const float* c = cs + 8 * (j & 7);
@@ -94,7 +96,7 @@ __device__ __forceinline__ nvk_u32x4 norm_rope8(nvk_u32x4 raw, nvk_u32x4 wraw, f
                           *reinterpret_cast<const nvk_u32x4*>(c + 4),
                           *reinterpret_cast<const nvk_u32x4*>(c + kHD / 2),
                           *reinterpret_cast<const nvk_u32x4*>(c + kHD / 2 + 4)};
-  return norm_rope8_cs(raw, wraw, eps, v, j);
+  return norm_rope8_cs<F16>(raw, wraw, eps, v, j);
 }
 
 }  // namespace nvk_qk

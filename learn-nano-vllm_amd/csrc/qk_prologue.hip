@@ -5,10 +5,11 @@
 // Semantics (nanovllm/models/qwen3.py:79-86 then attention.py:62-63):
 //   q, k, v = qkv.split([Hq*D, Hkv*D, Hkv*D], -1), viewed [T, H, D]
 //   q = RMSNorm(q) ; k = RMSNorm(k)                  (layernorm.py:16-26)
-//       x.float(); x *= rsqrt(mean(x^2) + eps); x = bf16(x) * weight (bf16)
+//       x.float(); x *= rsqrt(mean(x^2) + eps); x = T(x) * weight (T)
 //   q, k = rope(positions, q, k)                     (rotary_embedding.py:6-14, 37-48)
 //       x1, x2 = halves of x.float(); cos, sin = halves of cos_sin_cache[pos]
-//       y1 = x1*cos - x2*sin ; y2 = x2*cos + x1*sin ; bf16(cat(y1, y2))
+//       y1 = x1*cos - x2*sin ; y2 = x2*cos + x1*sin ; T(cat(y1, y2))
+// with T the model's element type, bf16 or f16 (model_runner.py:29).
 //   k_cache[slot] = k ; v_cache[slot] = v  for slot != -1  (attention.py:10-30)
 // Every f32 product and sum is rounded on its own (no fused multiply-add), as
 // the reference's separate tensor operations do.
@@ -87,6 +88,7 @@ constexpr int kRowsPerPass = 2;
 // One head row r of token t (uniform per 16-lane row group), its 16 bytes
 // `raw` already loaded; wq / wk: the lane's 8 norm weights of q / k, cs: its
 // cos and sin at the token's position.
+template <bool F16>
 __device__ __forceinline__ void prologue_row(const PrologueArgs& a, int64_t t, int r, int j,
                                              int32_t slot, nvk_u32x4 raw, nvk_u32x4 wq,
                                              nvk_u32x4 wk, const nvk_u32x4 (&cs)[4]) {
@@ -104,7 +106,7 @@ __device__ __forceinline__ void prologue_row(const PrologueArgs& a, int64_t t, i
     return;
   }
 
-  const nvk_u32x4 outw = nvk_qk::norm_rope8_cs(raw, is_q ? wq : wk, a.eps, cs, j);
+  const nvk_u32x4 outw = nvk_qk::norm_rope8_cs<F16>(raw, is_q ? wq : wk, a.eps, cs, j);
   if (is_q) {
     store_nt(a.q_out + t * a.q_out_stride_tok + (int64_t)r * a.q_out_stride_head + 8 * j, outw);
     return;
@@ -124,6 +126,7 @@ __device__ __forceinline__ void prologue_row(const PrologueArgs& a, int64_t t, i
 // weights and of the lane's cos/sin all leave before the first wait (left to
 // itself the compiler issues a row's load only after the previous row's
 // arithmetic and stores: two round trips for Qwen3's two rows per group).
+template <bool F16>
 __global__ __launch_bounds__(16 * kMaxRowGroups) void qk_prologue_kernel(PrologueArgs a) {
   const int64_t t = blockIdx.x;
   const int j = threadIdx.x & (kLanesPerRow - 1);
@@ -151,7 +154,7 @@ __global__ __launch_bounds__(16 * kMaxRowGroups) void qk_prologue_kernel(Prologu
       w = *reinterpret_cast<const nvk_u32x4*>((is_q ? a.q_weight : a.k_weight) + 8 * j);
       load_cs(cs);
     }
-    prologue_row(a, t, g, j, slot, raw, w, w, cs);
+    prologue_row<F16>(a, t, g, j, slot, raw, w, w, cs);
     return;
   }
   nvk_u32x4 cs[4];
@@ -169,7 +172,7 @@ __global__ __launch_bounds__(16 * kMaxRowGroups) void qk_prologue_kernel(Prologu
 #pragma unroll
     for (int i = 0; i < kRowsPerPass; ++i) {
       const int r = r0 + i * groups;
-      if (r < R) prologue_row(a, t, r, j, slot, raw[i], wq, wk, cs);
+      if (r < R) prologue_row<F16>(a, t, r, j, slot, raw[i], wq, wk, cs);
     }
   };
   if (R <= kRowsPerPass * groups) {  // one pass (Qwen3: 32 rows, 16 groups): no loop
@@ -189,7 +192,8 @@ extern "C" int nvk_qk_norm_rope_store(
     int64_t k_out_stride_tok, int64_t k_out_stride_head, void* k_cache, void* v_cache,
     const int32_t* slot_mapping, int64_t cache_slots, int32_t dtype, void* stream) {
   if (n_tokens < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || !(eps >= 0.f)) return NVK_EINVAL;
-  if (dtype != NVK_DTYPE_BF16 || head_dim != kHD) return NVK_EUNSUPPORTED;
+  if ((dtype != NVK_DTYPE_BF16 && dtype != NVK_DTYPE_F16) || head_dim != kHD)
+    return NVK_EUNSUPPORTED;
   if (n_tokens == 0) return NVK_OK;
   if (!qkv || !positions || !q_norm_weight || !k_norm_weight || !cos_sin_cache || !q_out)
     return NVK_EINVAL;
@@ -238,7 +242,12 @@ extern "C" int nvk_qk_norm_rope_store(
   a.v_cache = store ? static_cast<uint16_t*>(v_cache) : nullptr;
   a.slot_mapping = store ? slot_mapping : nullptr;
   a.cache_slots = cache_slots;
-  hipLaunchKernelGGL(qk_prologue_kernel, dim3((unsigned)n_tokens), dim3(groups * kLanesPerRow), 0,
-                     reinterpret_cast<hipStream_t>(stream), a);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == NVK_DTYPE_F16)
+    hipLaunchKernelGGL(qk_prologue_kernel<true>, dim3((unsigned)n_tokens),
+                       dim3(groups * kLanesPerRow), 0, st, a);
+  else
+    hipLaunchKernelGGL(qk_prologue_kernel<false>, dim3((unsigned)n_tokens),
+                       dim3(groups * kLanesPerRow), 0, st, a);
   return nvk_launch_status();
 }

@@ -46,6 +46,18 @@ def rope_cos_sin_cache(head_size: int, max_position: int, base: float,
     return cache if device is None else cache.to(device)
 
 
+def _same_dtype(*ts: torch.Tensor) -> None:
+    """qkv, the norm weights and the caches share the model's dtype (bf16 or
+    f16; model_runner.py:29 sets it for every parameter and the caches)."""
+    dt = ts[0].dtype
+    if dt not in (torch.bfloat16, torch.float16):
+        raise _lib.NvkError(f"the prologue is built for bfloat16 and float16, got {dt}")
+    for t in ts[1:]:
+        if t.dtype != dt:
+            raise _lib.NvkError(f"qkv, norm weights and caches must share one dtype: "
+                                f"{dt} and {t.dtype}")
+
+
 def qk_norm_rope_store(positions: torch.Tensor, qkv: torch.Tensor, num_heads: int,
                        num_kv_heads: int, head_dim: int, q_norm_weight: torch.Tensor,
                        k_norm_weight: torch.Tensor, eps: float, cos_sin_cache: torch.Tensor,
@@ -53,8 +65,9 @@ def qk_norm_rope_store(positions: torch.Tensor, qkv: torch.Tensor, num_heads: in
                        slot_mapping: torch.Tensor | None = None, return_k: bool = True):
     """q/k RMSNorm + RoPE + KV-store in one kernel.
 
-    positions: int64 [T]; qkv: bf16 [T, (num_heads + 2*num_kv_heads) * head_dim]
-    (last dim contiguous, any row stride).  Returns (q [T, Hq, D] new tensor,
+    positions: int64 [T]; qkv: bf16 or f16 (the model's dtype; the norm weights
+    and caches share it) [T, (num_heads + 2*num_kv_heads) * head_dim] (last
+    dim contiguous, any row stride).  Returns (q [T, Hq, D] new tensor,
     k [T, Hkv, D] new tensor or None when return_k is False, v = the view of
     qkv the reference passes on).  With slot_mapping given, the rotated k and
     the raw v rows are stored into the caches (slot -1 skipped), as
@@ -67,6 +80,7 @@ def qk_norm_rope_store(positions: torch.Tensor, qkv: torch.Tensor, num_heads: in
     assert q_norm_weight.numel() == head_dim and k_norm_weight.numel() == head_dim
     cs = cos_sin_cache.reshape(cos_sin_cache.shape[0], -1)
     assert cs.shape[1] == head_dim and cs.stride(-1) == 1 and cs.dtype == torch.float32
+    _same_dtype(qkv, q_norm_weight, k_norm_weight)
     v = qkv[:, q_size + kv_size:].view(-1, num_kv_heads, head_dim)
     store = slot_mapping is not None
     if store:
@@ -75,7 +89,8 @@ def qk_norm_rope_store(positions: torch.Tensor, qkv: torch.Tensor, num_heads: in
         assert k_cache.stride(1) == D and v_cache.stride(1) == D      # attention.py:38
         assert slot_mapping.numel() == T                               # attention.py:39
         assert k_cache.stride(0) == k_cache.shape[1] * D and v_cache.stride(0) == v_cache.shape[1] * D
-        assert k_cache.shape == v_cache.shape and k_cache.dtype == qkv.dtype == v_cache.dtype
+        assert k_cache.shape == v_cache.shape
+        _same_dtype(qkv, k_cache, v_cache)
     dev = _lib.require_gpu(qkv, positions, q_norm_weight, k_norm_weight, cs,
                            k_cache if store else None, v_cache if store else None, slot_mapping)
     q = torch.empty(T, num_heads, head_dim, dtype=qkv.dtype, device=dev)
@@ -123,6 +138,7 @@ def paged_decode_with_prologue(positions: torch.Tensor, qkv: torch.Tensor, num_h
     assert q_norm_weight.numel() == head_dim and k_norm_weight.numel() == head_dim
     cs = cos_sin_cache.reshape(cos_sin_cache.shape[0], -1)
     assert cs.shape[1] == head_dim and cs.stride(-1) == 1 and cs.dtype == torch.float32
+    _same_dtype(qkv, q_norm_weight, k_norm_weight, k_cache, v_cache)
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()) or k_cache.shape != v_cache.shape:
         raise _lib.NvkError("k_cache/v_cache must be contiguous [num_blocks, block_size, Hkv, D]")
     num_blocks, block_size, hkv, dk = k_cache.shape

@@ -18,6 +18,7 @@ What it restates (numpy, bf16 carried as uint16 bit patterns):
   slots_for         the slot formula slot = bt[p // bs] * bs + p % bs used by
                     model_runner.py:151-161, 181.
   rms_norm          RMSNorm.rms_forward, nanovllm/layers/layernorm.py:16-26
+                    (bf16 or f16 elements, the model's dtype, model_runner.py:29)
   apply_rotary_emb  rotary_embedding.py:6-14 (x.float(), halves, separately
                     rounded f32 products, bf16 result)
   qk_norm_rope_store  the prologue of Qwen3Attention.forward,
@@ -203,27 +204,44 @@ def paged_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, cu_seqlens_q, s
 # ---------------------------------------------------------------------------
 # Attention prologue: q/k RMSNorm + RoPE (+ the KV store)
 # ---------------------------------------------------------------------------
+def f16_to_f32(u16: np.ndarray) -> np.ndarray:
+    """float16 bit patterns (uint16) -> float32 (exact)."""
+    return np.asarray(u16, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    """float32 -> float16 bit patterns, round to nearest even."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+# 16-bit element types of the model (model_runner.py:29): widen, round
+_ELT = {"bf16": (bf16_to_f32, f32_to_bf16), "f16": (f16_to_f32, f32_to_f16)}
+
+
 def rms_norm(x_bits: np.ndarray, weight_bits: np.ndarray, eps: float,
-             _mutation: str | None = None) -> np.ndarray:
-    """RMSNorm over the last dim, bf16 in / bf16 out (layernorm.py:16-26):
-    x = x.float(); x *= rsqrt(mean(x^2) + eps); x = bf16(x) * weight -> bf16.
+             _mutation: str | None = None, elt: str = "bf16") -> np.ndarray:
+    """RMSNorm over the last dim, T in / T out (layernorm.py:16-26), T the
+    element type `elt` ("bf16" or "f16", bit patterns as uint16):
+    x = x.float(); x *= rsqrt(mean(x^2) + eps); x = T(x) * weight -> T.
     rsqrt is evaluated in float64 and rounded once to float32."""
-    x = bf16_to_f32(x_bits)
+    widen, narrow = _ELT[elt]
+    x = widen(x_bits)
     var = np.mean(x * x, axis=-1, keepdims=True, dtype=np.float32)
     if _mutation == "sum":
         var = np.sum(x * x, axis=-1, keepdims=True, dtype=np.float32)
     rstd = (1.0 / np.sqrt((var + np.float32(eps)).astype(np.float64))).astype(np.float32)
-    normed = f32_to_bf16(x * rstd)
-    w = bf16_to_f32(weight_bits)
-    return f32_to_bf16(bf16_to_f32(normed) * w)
+    normed = narrow(x * rstd)
+    w = widen(weight_bits)
+    return narrow(widen(normed) * w)
 
 
 def apply_rotary_emb(x_bits: np.ndarray, cos: np.ndarray, sin: np.ndarray,
-                     _mutation: str | None = None) -> np.ndarray:
+                     _mutation: str | None = None, elt: str = "bf16") -> np.ndarray:
     """rotary_embedding.py:6-14: x1, x2 = halves of x.float();
     y1 = x1*cos - x2*sin, y2 = x2*cos + x1*sin (each product and sum rounded to
-    float32), cat -> bf16.  cos/sin broadcast against x's halves."""
-    x = bf16_to_f32(x_bits)
+    float32), cat -> T (`elt`).  cos/sin broadcast against x's halves."""
+    widen, narrow = _ELT[elt]
+    x = widen(x_bits)
     h = x.shape[-1] // 2
     if _mutation == "interleaved":
         x1, x2 = x[..., 0::2], x[..., 1::2]
@@ -240,16 +258,17 @@ def apply_rotary_emb(x_bits: np.ndarray, cos: np.ndarray, sin: np.ndarray,
     if _mutation == "interleaved":
         y = np.empty_like(x)
         y[..., 0::2], y[..., 1::2] = y1, y2
-        return f32_to_bf16(y)
-    return f32_to_bf16(np.concatenate([y1, y2], axis=-1))
+        return narrow(y)
+    return narrow(np.concatenate([y1, y2], axis=-1))
 
 
 def qk_norm_rope_store(qkv_bits: np.ndarray, positions, q_weight_bits: np.ndarray,
                        k_weight_bits: np.ndarray, eps: float, cos_sin: np.ndarray,
                        num_q_heads: int, num_kv_heads: int, head_dim: int,
                        k_cache: np.ndarray | None = None, v_cache: np.ndarray | None = None,
-                       slot_mapping=None):
-    """qwen3.py:79-86 + attention.py:62-63 on bf16 bit patterns.
+                       slot_mapping=None, elt: str = "bf16"):
+    """qwen3.py:79-86 + attention.py:62-63 on bit patterns of the element type
+    `elt` ("bf16" or "f16").
 
     qkv_bits [T, (Hq + 2*Hkv)*D]; cos_sin float32 [max_position, D] (cos | sin
     halves).  Returns (q [T,Hq,D], k [T,Hkv,D], v [T,Hkv,D]) as uint16; with
@@ -259,12 +278,12 @@ def qk_norm_rope_store(qkv_bits: np.ndarray, positions, q_weight_bits: np.ndarra
     q = qkv_bits[:, :qs].reshape(t, num_q_heads, head_dim)
     k = qkv_bits[:, qs:qs + ks].reshape(t, num_kv_heads, head_dim)
     v = np.ascontiguousarray(qkv_bits[:, qs + ks:qs + 2 * ks]).reshape(t, num_kv_heads, head_dim)
-    q = rms_norm(q, q_weight_bits, eps)
-    k = rms_norm(k, k_weight_bits, eps)
+    q = rms_norm(q, q_weight_bits, eps, elt=elt)
+    k = rms_norm(k, k_weight_bits, eps, elt=elt)
     cs = np.asarray(cos_sin, dtype=np.float32)[np.asarray(positions, dtype=np.int64)]
     cos, sin = cs[:, None, :head_dim // 2], cs[:, None, head_dim // 2:]
-    q = apply_rotary_emb(q, cos, sin)
-    k = apply_rotary_emb(k, cos, sin)
+    q = apply_rotary_emb(q, cos, sin, elt=elt)
+    k = apply_rotary_emb(k, cos, sin, elt=elt)
     if k_cache is not None and slot_mapping is not None:
         kv_store(k, v, k_cache, v_cache, slot_mapping)
     return q, k, v

@@ -38,19 +38,22 @@ def assert_attn_close(out: torch.Tensor, ref: np.ndarray, what: str = "") -> Non
     torch.testing.assert_close(got, exp, atol=ATOL, rtol=RTOL, msg=lambda m: f"{what}: {m}")
 
 
-def assert_rotated_close(got_bits: np.ndarray, ref_bits: np.ndarray, what: str = "") -> None:
-    """Normed + rotated bf16 rows (last dim D) against the oracle: bit-exact but
-    for < 0.1 % of elements where sum-of-squares / rsqrt rounding moved a
-    normed value across a bf16 rounding boundary, which stay within 2 bf16
-    ulps of the rotated pair, |diff| <= 2^-6 * (|x1| + |x2|)."""
-    got = orc.bf16_to_f32(got_bits).astype(np.float64)
-    ref = orc.bf16_to_f32(ref_bits).astype(np.float64)
+def assert_rotated_close(got_bits: np.ndarray, ref_bits: np.ndarray, what: str = "",
+                         elt: str = "bf16") -> None:
+    """Normed + rotated rows (last dim D) of element type `elt` against the
+    oracle: bit-exact but for < 0.1 % of elements where sum-of-squares / rsqrt
+    rounding moved a normed value across a rounding boundary of the type,
+    which stay within 2 ulps of the rotated pair, |diff| <= 2^-6 (bf16) or
+    2^-9 (f16) * (|x1| + |x2|)."""
+    widen = orc.bf16_to_f32 if elt == "bf16" else orc.f16_to_f32
+    got = widen(got_bits).astype(np.float64)
+    ref = widen(ref_bits).astype(np.float64)
     same = got_bits == ref_bits
     assert same.mean() > 0.999, f"{what}: {(~same).sum()} of {same.size} differ"
     h = ref.shape[-1] // 2
     scale = np.abs(ref[..., :h]) + np.abs(ref[..., h:])
     scale = np.concatenate([scale, scale], axis=-1)
-    bad = np.abs(got - ref) > 2.0 ** -6 * scale + 1e-30
+    bad = np.abs(got - ref) > (2.0 ** -6 if elt == "bf16" else 2.0 ** -9) * scale + 1e-30
     assert not bad.any(), f"{what}: {bad.sum()} elements beyond 2 bf16 ulps"
 
 

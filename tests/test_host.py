@@ -106,7 +106,7 @@ def test_error_codes_without_launching():
     pro = [16, 32 * 128, 4, 16, 16, 16, 1e-6, 16, 128, 4096, 16, 8, 128, 16, 16 * 128, 128,
            None, 0, 0, 16, 16, 16, 1 << 20, 0, None]
     assert lib.nvk_qk_norm_rope_store(*pro[:12], 64, *pro[13:]) == -2     # head_dim 64
-    assert lib.nvk_qk_norm_rope_store(*pro[:23], 1, None) == -2           # fp16
+    assert lib.nvk_qk_norm_rope_store(*pro[:23], 2, None) == -2           # f32 (bf16, f16 built)
     zero = list(pro); zero[2] = 0
     assert lib.nvk_qk_norm_rope_store(*zero) == 0                          # nothing to do
     no_q = list(pro); no_q[13] = None
@@ -126,8 +126,8 @@ def test_error_codes_without_launching():
           128, 256, 8, 1024, 0.088, 16, 16 * 128, 128, 16, 1 << 30, 0, None]
     hd64 = list(dp); hd64[19] = 64
     assert lib.nvk_paged_decode_prologue(*hd64) == -2                     # head_dim 64
-    fp16 = list(dp); fp16[29] = 1
-    assert lib.nvk_paged_decode_prologue(*fp16) == -2
+    f32 = list(dp); f32[29] = 2
+    assert lib.nvk_paged_decode_prologue(*f32) == -2                      # f32 (bf16, f16 built)
     none = list(dp); none[16] = 0
     assert lib.nvk_paged_decode_prologue(*none) == 0                      # empty batch
     no_slots = list(dp); no_slots[11] = None

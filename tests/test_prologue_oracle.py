@@ -178,3 +178,83 @@ def test_qk_norm_rope_store_matches_per_token_loop(cos_sin):
             exp_vc[slots[i]] = row[hq + hkv:]
     assert np.array_equal(kc.reshape(nb * bs, hkv, D), exp_kc)
     assert np.array_equal(vc.reshape(nb * bs, hkv, D), exp_vc)
+
+
+# --------------------------------------------------------------------------- f16
+# The reference runs the model in hf_config.dtype (model_runner.py:29), so the
+# prologue also exists for float16: the same operations with every rounding
+# to T done to float16.
+def _rand_f16(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.float16)
+
+
+def test_rms_norm_f16_matches_transformers_qwen3_rmsnorm():
+    m = _transformers()
+    x = _rand_f16((257, 4, D), 20, scale=3.0)
+    w = _weight(21).to(torch.float16)
+    norm = m.Qwen3RMSNorm(D, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(w.float())
+        norm = norm.to(torch.float16)
+        ref = _bits(norm(x))
+    got = orc.rms_norm(_bits(x), _bits(w), 1e-6, elt="f16")
+    same = got == ref
+    assert same.mean() > 0.999
+    diff = np.abs(orc.f16_to_f32(got) - orc.f16_to_f32(ref))
+    assert np.all(diff <= np.abs(orc.f16_to_f32(ref)) * 2.0 ** -9)
+    # rounding to bf16 instead of f16 (a planted mistake) is far from it
+    wrong = orc.rms_norm(_bits(x), _bits(w.to(torch.bfloat16)), 1e-6)
+    assert (orc.bf16_to_f32(wrong) != orc.f16_to_f32(ref)).mean() > 0.5
+
+
+def test_rms_norm_f16_closed_forms():
+    x = _bits(_rand_f16((64, D), 22))
+    one = _bits(torch.ones(D, dtype=torch.float16))
+    x2 = orc.f32_to_f16(orc.f16_to_f32(x) * 4.0)          # exact in f16
+    assert np.array_equal(orc.rms_norm(x2, one, 0.0, elt="f16"),
+                          orc.rms_norm(x, one, 0.0, elt="f16"))
+    xn = x ^ np.uint16(0x8000)
+    assert np.array_equal(orc.rms_norm(xn, one, 0.0, elt="f16"),
+                          orc.rms_norm(x, one, 0.0, elt="f16") ^ np.uint16(0x8000))
+    y = orc.f16_to_f32(orc.rms_norm(x, one, 1e-6, elt="f16"))
+    np.testing.assert_allclose(np.mean(y * y, axis=-1), 1.0, rtol=2e-3)
+
+
+def test_rope_f16_matches_transformers_bit_for_bit(cos_sin):
+    m = _transformers()
+    x = _rand_f16((300, 3, D), 23)
+    pos = np.random.default_rng(24).integers(0, MAX_POS, 300)
+    cs = torch.from_numpy(cos_sin[pos])
+    c, s = cs[:, :D // 2], cs[:, D // 2:]
+    xf = x.float()
+    q_embed, _ = m.apply_rotary_pos_emb(xf, xf, torch.cat((c, c), -1), torch.cat((s, s), -1),
+                                        unsqueeze_dim=1)
+    got = orc.apply_rotary_emb(_bits(x), cos_sin[pos][:, None, :D // 2],
+                               cos_sin[pos][:, None, D // 2:], elt="f16")
+    assert np.array_equal(got, _bits(q_embed.to(torch.float16)))
+    ident = orc.apply_rotary_emb(_bits(x), cos_sin[[0] * 300][:, None, :D // 2],
+                                 cos_sin[[0] * 300][:, None, D // 2:], elt="f16")
+    assert np.array_equal(ident, _bits(x))
+
+
+def test_qk_norm_rope_store_f16_matches_per_token_loop(cos_sin):
+    hq, hkv, t = 4, 2, 7
+    qkv = _bits(_rand_f16((t, (hq + 2 * hkv) * D), 25, scale=2.0))
+    qw, kw = _bits(_weight(26).to(torch.float16)), _bits(_weight(27).to(torch.float16))
+    pos = np.array([5, 6, 7, 0, 1, 300, 39999])
+    kc = np.zeros((2, 8, hkv, D), dtype=np.uint16)
+    vc = np.zeros_like(kc)
+    slots = np.array([3, -1, 15, 0, 7, 9, 1])
+    q, k, v = orc.qk_norm_rope_store(qkv, pos, qw, kw, 1e-6, cos_sin, hq, hkv, D, kc, vc, slots,
+                                     elt="f16")
+    for i in range(t):
+        row = qkv[i].reshape(hq + 2 * hkv, D)
+        cs = cos_sin[pos[i]]
+        for h in range(hq + hkv):
+            n = orc.rms_norm(row[h][None], qw if h < hq else kw, 1e-6, elt="f16")
+            r = orc.apply_rotary_emb(n, cs[None, :D // 2], cs[None, D // 2:], elt="f16")[0]
+            assert np.array_equal(q[i, h] if h < hq else k[i, h - hq], r), (i, h)
+        if slots[i] >= 0:
+            assert np.array_equal(kc.reshape(16, hkv, D)[slots[i]], k[i])
+            assert np.array_equal(vc.reshape(16, hkv, D)[slots[i]], row[hq + hkv:])
