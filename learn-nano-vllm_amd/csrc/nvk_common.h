@@ -180,3 +180,23 @@ static inline int nvk_log2_exact(int v) {
   while ((1 << s) < v) ++s;
   return s;
 }
+
+// ---- stream-K bookkeeping ----------------------------------------------------
+// Last b in [0, B) with n * s_cs[b] <= c (s_cs non-decreasing, s_cs[0] = 0,
+// c >= 0; B <= 4096), wave-uniform: the 64 lanes test every (B/64)-th entry,
+// a ballot keeps the last that holds, and a second round tests the entries
+// after it.  Two dependent LDS reads instead of a binary search's log2 B.
+NVK_DEVICE int nvk_last_le(const int* s_cs, int B, int n, int64_t c, int lane) {
+  const int stride = (B + 63) / 64;
+  int b = lane * stride;
+  bool p = b < B && (int64_t)n * s_cs[b] <= c;
+  uint64_t m = __builtin_amdgcn_ballot_w64(p);  // lane 0 holds: s_cs[0] = 0
+  int lo = (63 - __builtin_clzll(m)) * stride;
+  if (stride > 1) {
+    b = lo + lane;
+    p = lane < stride && b < B && (int64_t)n * s_cs[b] <= c;
+    m = __builtin_amdgcn_ballot_w64(p);  // lane 0 (b = lo) holds
+    lo += 63 - __builtin_clzll(m);
+  }
+  return __builtin_amdgcn_readfirstlane(lo);
+}

@@ -135,8 +135,9 @@ __device__ __forceinline__ float xor_lane(float x, int mask) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(x)));
 }
 
-// Exclusive prefix of chunks per sequence into s_cs[0..B]; returns the total.
-__device__ int chunk_prefix(const DecodeArgs& a, int* s_cs, int* s_wsum) {
+// Exclusive prefix of chunks per sequence into s_cs[0..B] and the clamped
+// context lengths into s_ctx[0..B); returns the total.
+__device__ int chunk_prefix(const DecodeArgs& a, int* s_cs, int* s_ctx, int* s_wsum) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int B = a.batch;
   const int per = (B + 255) / 256;
@@ -144,7 +145,11 @@ __device__ int chunk_prefix(const DecodeArgs& a, int* s_cs, int* s_wsum) {
   int local = 0;
   for (int i = 0; i < per; ++i) {
     const int b = b0 + i;
-    if (b < B) local += (clamp_ctx(a, b) + a.tc - 1) / a.tc;
+    if (b < B) {
+      const int ctx = clamp_ctx(a, b);
+      s_ctx[b] = ctx;
+      local += (ctx + a.tc - 1) / a.tc;
+    }
   }
   int x = local;
 #pragma unroll
@@ -161,7 +166,7 @@ __device__ int chunk_prefix(const DecodeArgs& a, int* s_cs, int* s_wsum) {
     const int b = b0 + i;
     if (b < B) {
       s_cs[b] = run;
-      run += (clamp_ctx(a, b) + a.tc - 1) / a.tc;
+      run += (s_ctx[b] + a.tc - 1) / a.tc;
     }
   }
   const int total = s_wsum[0] + s_wsum[1] + s_wsum[2] + s_wsum[3];
@@ -403,11 +408,53 @@ __device__ __forceinline__ void compute_chunk(const DecodeArgs& a, const ChunkBu
   }
 }
 
+// x combined (max or sum) with lane l ^ S, for S in {8, 16, 32}, by VALU
+// exchanges (a DPP row rotation by 8, v_permlane16_swap, v_permlane32_swap)
+// instead of an LDS round trip.  Both lanes of a pair get op(even, odd):
+// the same value as op(x, x of lane l ^ S), op being commutative.
+template <int S, bool MAX>
+__device__ __forceinline__ float pair_op(float x) {
+  float a, b;
+  if constexpr (S == 8) {
+    a = x;
+    b = nvk_dpp<NVK_DPP_ROW_ROR8>(x);  // row_ror:8: lane l ^ 8 of the 16-lane row
+  } else {
+    const auto r = S == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x),
+                                                                __float_as_uint(x), false, false)
+                           : __builtin_amdgcn_permlane32_swap(__float_as_uint(x),
+                                                                __float_as_uint(x), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  }
+  return MAX ? fmaxf(a, b) : a + b;
+}
+// op over the row groups LPR, 2 LPR, ... apart (HPI = 1: all of a wave's
+// row groups hold the same kv head)
+template <int LPR, bool MAX>
+__device__ __forceinline__ float rows_op(float x) {
+  if constexpr (LPR <= 8) x = pair_op<8, MAX>(x);
+  if constexpr (LPR <= 16) x = pair_op<16, MAX>(x);
+  return pair_op<32, MAX>(x);
+}
+
 // Merges the row groups that hold the same kv head (they differ by multiples
 // of `stride` lanes; `tpi` of them).  Afterwards the lanes with tt == 0 hold
-// the head's state.
-template <int G>
+// the head's state.  One kv head per load instruction (the library's choice,
+// decode_hpi): VALU lane exchanges; otherwise LDS permutes.
+template <int G, int LPR>
 __device__ __forceinline__ void merge_same_head(SoftmaxState<G>& st, int tpi, int stride) {
+  if (stride == LPR && stride * tpi == 64) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float M = rows_op<LPR, true>(st.m[h]);
+      const float w = (M == -INFINITY) ? 0.f : nvk_fast_exp2(st.m[h] - M);
+      st.l[h] = rows_op<LPR, false>(st.l[h] * w);
+      st.m[h] = M;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) st.o[h][e] = rows_op<LPR, false>(st.o[h][e] * w);
+    }
+    return;
+  }
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     float M = st.m[h];
@@ -443,6 +490,9 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   constexpr int RPI = 64 / CB::LPR;           // head rows per load instruction
   constexpr int REC_HEAD = G * (HD + 4);      // floats per head in a record
   __shared__ int s_cs[kMaxBatch + 1];
+  // context lengths, read once per workgroup: a wave that moves to another
+  // sequence finds its length here instead of in a dependent global load
+  __shared__ int s_ctx[kMaxBatch];
   __shared__ int s_wsum[kWavesPerWG];
   __shared__ nvk_u32x4 s_q[FUSED ? kWavesPerWG * G * nvk_qk::kLanesPerRow : 1];
 
@@ -457,7 +507,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   role.tt = g / hpi;
   const int n_blk = a.num_kv_heads / hpi;
 
-  const int S = chunk_prefix(a, s_cs, s_wsum);
+  const int S = chunk_prefix(a, s_cs, s_ctx, s_wsum);
   if (blockIdx.x == 0) {  // empty contexts: no wave visits them
     for (int e = tid; e < a.batch * n_blk; e += 256) {
       const int b = e / n_blk;
@@ -474,19 +524,14 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
   if (c0 >= c1) return;
 
   // locate chunk c0: last b with n_blk*s_cs[b] <= c0
-  int lo = 0, hi = a.batch - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if ((int64_t)n_blk * uniform(s_cs[mid]) <= c0) lo = mid; else hi = mid - 1;
-  }
   ChunkPos cur;
-  cur.b = uniform(lo);
+  cur.b = nvk_last_le(s_cs, a.batch, n_blk, c0, lane);
   cur.n = uniform(s_cs[cur.b + 1] - s_cs[cur.b]);
   const int r = (int)(c0 - (int64_t)n_blk * s_cs[cur.b]);
   cur.blk = uniform(r / cur.n);
   cur.k = uniform(r % cur.n);
   bool started_here = cur.k == 0;
-  int ctx = clamp_ctx(a, cur.b);
+  int ctx = uniform(s_ctx[cur.b]);
   // fused: the new token's position (a scalar read beside the context length)
   int64_t pos = FUSED ? ((nvk_const_i64*)a.positions)[cur.b] : 0;
   int slot = FUSED ? ((nvk_const_i32*)a.slot_mapping)[cur.b] : -1;
@@ -518,7 +563,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     const bool last = c + 1 == c1;
     const bool group_end = cur.k == cur.n - 1;
     if (group_end || last) {
-      if (tpi > 1) merge_same_head<G>(st, tpi, hpi * CB::LPR);
+      if (tpi > 1) merge_same_head<G, CB::LPR>(st, tpi, hpi * CB::LPR);
       const int kvh = cur.blk * hpi + role.hh;
       const bool whole = group_end && started_here;
       if (role.tt == 0) {
@@ -559,7 +604,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     const int b_prev = cur.b;
     advance(cur, s_cs, n_blk);
     if (cur.b != b_prev) {
-      ctx = clamp_ctx(a, cur.b);
+      ctx = uniform(s_ctx[cur.b]);
       if constexpr (FUSED) {
         pos = ((nvk_const_i64*)a.positions)[cur.b];
         slot = ((nvk_const_i32*)a.slot_mapping)[cur.b];

@@ -190,12 +190,7 @@ __global__ __launch_bounds__(64 * kWavesPerWG, 2) void short_query_kernel(SqArgs
   if (c0 >= c1) return;
 
   // first chunk: last sequence s with Hkv * s_cs[s] <= c0
-  int lo = 0, hi = a.p.batch - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if ((int64_t)Hkv * uniform(s_cs[mid]) <= c0) lo = mid; else hi = mid - 1;
-  }
-  int s = uniform(lo);
+  int s = nvk_last_le(s_cs, a.p.batch, Hkv, c0, lane);
   int n = uniform(s_cs[s + 1] - s_cs[s]);
   int kvh, k;
   {
