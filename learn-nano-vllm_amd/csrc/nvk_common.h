@@ -200,3 +200,17 @@ NVK_DEVICE int nvk_last_le(const int* s_cs, int B, int n, int64_t c, int lane) {
   }
   return __builtin_amdgcn_readfirstlane(lo);
 }
+
+// Inclusive prefix sum over the 64 lanes of a wave in six DPP adds (row
+// shifts by 1, 2, 4, 8 inside each 16-lane row, then the row totals carried
+// by row_bcast:15 and row_bcast:31), no LDS round trip.  Equal to the
+// __shfl_up scan for every input (integer adds).
+NVK_DEVICE int nvk_wave_scan_add(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
+  return x;
+}

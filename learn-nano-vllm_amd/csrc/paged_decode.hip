@@ -151,12 +151,7 @@ __device__ int chunk_prefix(const DecodeArgs& a, int* s_cs, int* s_ctx, int* s_w
       local += (ctx + a.tc - 1) / a.tc;
     }
   }
-  int x = local;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off);
-    if (lane >= off) x += y;
-  }
+  const int x = nvk_wave_scan_add(local);  // inclusive over the wave
   if (lane == 63) s_wsum[wave] = x;
   __syncthreads();
   int base = 0;

@@ -102,12 +102,7 @@ __device__ int chunk_prefix(const SqArgs& a, int* s_cs, int* s_wsum) {
   int local = 0;
   for (int i = 0; i < per; ++i)
     if (b0 + i < B) local += seq_chunks(a, b0 + i);
-  int x = local;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off);
-    if (lane >= off) x += y;
-  }
+  const int x = nvk_wave_scan_add(local);  // inclusive over the wave
   if (lane == 63) s_wsum[wave] = x;
   __syncthreads();
   int run = x - local;

@@ -10,7 +10,7 @@ import torch
 from torch import nn
 
 from nanovllm_amd import _lib
-from nanovllm_amd.flash_api import varlen_prefill, paged_decode
+from nanovllm_amd.flash_api import paged_decode, prefill_tile_order, varlen_prefill
 from nanovllm_amd.utils.context import get_context
 
 
@@ -45,6 +45,33 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
     _lib.check(code)
 
 
+# The longest-first tile order of the current step's prefill, ranked by the
+# first layer and reused by the others: every layer of a step reads the same
+# Context (one set_context per step, model_runner.py:132-169), so the order
+# is keyed on the step's cu_seqlens tensors and the call's sizes.  Any order
+# gives the same output bits (an order of other sizes is ignored by the
+# kernel), so a stale entry can only cost time.
+_step_order: list = [None, None]     # [key, order tensor or None]
+
+
+def _prefill_order(context, q, k, block_table):
+    if torch.cuda.is_current_stream_capturing():
+        return None                      # no cached device buffer inside a graph
+    hkv = k.shape[2] if block_table is not None else k.shape[1]
+    key = (context.cu_seqlens_q, context.cu_seqlens_k, context.max_seqlen_q,
+           context.max_seqlen_k, q.shape[1], hkv, k.shape[1] if block_table is not None else 0,
+           block_table.shape[1] if block_table is not None else k.shape[0], q.device)
+    cached = _step_order[0]
+    if cached is not None and len(cached) == len(key) and all(
+            a is b if isinstance(a, torch.Tensor) else a == b for a, b in zip(cached, key)):
+        return _step_order[1]
+    order = prefill_tile_order(context.cu_seqlens_q, context.cu_seqlens_k, context.max_seqlen_q,
+                               k, q.shape[1], block_table=block_table,
+                               max_seqlen_k=context.max_seqlen_k)
+    _step_order[0], _step_order[1] = key, order
+    return order
+
+
 class Attention(nn.Module):
     """Same constructor and forward as nanovllm.layers.attention.Attention.
 
@@ -71,9 +98,10 @@ class Attention(nn.Module):
         if context.is_prefill:
             if context.block_tables is not None:    # prefix cache / later chunk
                 k, v = k_cache, v_cache
+            order = _prefill_order(context, q, k, context.block_tables)
             o = varlen_prefill(q, k, v, context.cu_seqlens_q, context.cu_seqlens_k,
                                context.max_seqlen_q, self.scale, block_table=context.block_tables,
-                               max_seqlen_k=context.max_seqlen_k)
+                               max_seqlen_k=context.max_seqlen_k, order=order)
         else:    # decode
             o = paged_decode(q, k_cache, v_cache, context.context_lens, context.block_tables,
                              self.scale).unsqueeze(1)

@@ -115,3 +115,55 @@ def test_attention_module_end_to_end():
     reset_context()
     # the other layer's cache view was never written
     assert kv_cache[:, 0].eq(0).all()
+
+
+def test_layers_of_a_step_share_one_tile_order():
+    """A chunked-prefill step through three Attention layers (their own cache
+    views, one Context): the first layer ranks the query tiles, the other
+    two reuse that order, and each output equals varlen_prefill ranking its
+    own tiles, bit for bit.  A new step (new Context) ranks again."""
+    from nanovllm_amd import varlen_prefill
+    from nanovllm_amd.layers import attention as attn_mod
+    gen = torch.Generator().manual_seed(33)
+    Sequence.block_size = BS
+    nb, layers = 120, 3
+    kv_cache = torch.randn(2, layers, nb, BS, HKV, HD, generator=gen).to(torch.bfloat16).cuda()
+    mods = []
+    for i in range(layers):
+        m = Attention(HQ, HD, HD ** -0.5, HKV)
+        m.k_cache, m.v_cache = kv_cache[0, i], kv_cache[1, i]
+        mods.append(m)
+    rng = np.random.default_rng(34)
+    perm = rng.permutation(nb).tolist()
+    seqs, nxt = [], 0
+    for _ in range(24):
+        cached = int(rng.integers(1, 3)) * BS
+        new = int(rng.integers(40, 500)) if seqs else 500
+        pages = (cached + new + BS - 1) // BS
+        seqs.append(Sequence(list(range(cached + new)), block_table=perm[nxt:nxt + pages],
+                             num_cached_tokens=cached, num_scheduled_tokens=new))
+        nxt += pages
+    metadata.prepare_prefill(seqs, BS)
+    ctx = get_context()
+    assert ctx.block_tables is not None
+    # enough query tiles (24 sequences x 8 tiles x 8 kv heads) for a ranked order
+    assert len(seqs) == 24 and ctx.max_seqlen_q > 7 * 64
+    n = sum(s.num_scheduled_tokens for s in seqs)
+    orders = []
+    try:
+        for i, m in enumerate(mods):
+            q, k, v = _qkv(n, gen)
+            say(f"module layer {i} of a chunked-prefill step")
+            o = m(q, k, v)
+            orders.append(attn_mod._step_order[1])
+            ref = varlen_prefill(q, m.k_cache, m.v_cache, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
+                                 ctx.max_seqlen_q, HD ** -0.5, block_table=ctx.block_tables,
+                                 max_seqlen_k=ctx.max_seqlen_k)
+            torch.cuda.synchronize()
+            assert torch.equal(o, ref), f"layer {i}"
+        assert orders[0] is not None and orders[1] is orders[0] and orders[2] is orders[0]
+        metadata.prepare_prefill(seqs, BS)       # the next step: new cu_seqlens tensors
+        mods[0](*_qkv(n, gen))
+        assert attn_mod._step_order[1] is not orders[0]
+    finally:
+        reset_context()
