@@ -545,15 +545,19 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
   float l_part[2] = {0.f, 0.f};  // this lane's share of the row sum (two chains)
 
   // Scores of keys a row may not see -> -inf (boundary tiles only; uniform).
+  // Score i of block mb is key kbase + 4 half + c with the constant c below:
+  // it stays iff c <= min(row_limit, n_keys - 1) - kbase - 4 half, one
+  // compare and one select per score.
   auto mask_tile = [&](nvk_f32x16 (&sc)[2], int kt) {
     const int kbase = kt * kKeys;
     if (kbase + kKeys > unmasked_keys || kbase + kKeys > n_keys) {
+      const int lim = (row_limit < n_keys - 1 ? row_limit : n_keys - 1) - kbase - 4 * half;
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int key = kbase + 32 * mb + 8 * (i >> 2) + 4 * half + (i & 3);
-          sc[mb][i] = (key <= row_limit && key < n_keys) ? sc[mb][i] : -INFINITY;
+          const int c = 32 * mb + 8 * (i >> 2) + (i & 3);
+          sc[mb][i] = c <= lim ? sc[mb][i] : -INFINITY;
         }
       }
     }
@@ -824,6 +828,11 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       max_join_a(sc, ch, tj);
       mt = max_join_b(sc, tj);
     }
+    // The first tile sets the reference max: the accumulators and row sums
+    // are still zero, so the rescale the first step would run (alpha = 0)
+    // changes nothing and is skipped.  A row that sees no key of the tile
+    // keeps -inf.
+    m_ref = mt;
     auto step = [&](auto par, int kt) {
       constexpr int P = decltype(par)::value;
       wait_lds_loads();
