@@ -761,42 +761,52 @@ def copy_ceiling(torch, dev, nbytes, args):
 PROBE_LIB = os.path.join(ROOT, "learn-nano-vllm_amd", "bench_probe", "libnvk_probe.so")
 
 
-def stream_ceilings(torch, dev, args, store_bytes=None):
-    """GB/s that plain streaming kernels reach on this box (hand-written, 16 B
-    per lane, non-temporal; learn-nano-vllm_amd/bench_probe/stream_probe.hip):
-    read-only, write-only and copy over 512 MiB buffers, and a copy of the
-    store's own byte count, each under the >= 1 GiB rotation of the legs.
-    These are the rates a read + write kernel (the store, the prologue) and a
-    read kernel (the decode) can be held against, besides the 8 TB/s peak."""
+def stream_probe_rate(torch, dev, args, mode, nbytes, moved):
+    """GB/s (of `moved` bytes per launch) of one hand-written streaming kernel
+    (learn-nano-vllm_amd/bench_probe/stream_probe.hip: 16 B per lane,
+    non-temporal): mode 0 reads `nbytes`, 1 writes them, 2 copies them; timed
+    like the legs, over buffers rotated past the >= 1 GiB of the caches."""
     import ctypes
     lib = ctypes.CDLL(PROBE_LIB)
     lib.nvk_probe_stream.restype = ctypes.c_int
     lib.nvk_probe_stream.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
                                      ctypes.c_size_t, ctypes.c_void_p]
 
-    def call(mode, a, b, n):
-        rc = lib.nvk_probe_stream(mode, a.data_ptr() if a is not None else None, b.data_ptr(), n,
-                                  torch.cuda.current_stream(dev).cuda_stream)
+    def call(a, b):
+        rc = lib.nvk_probe_stream(mode, a.data_ptr() if a is not None else None, b.data_ptr(),
+                                  nbytes, torch.cuda.current_stream(dev).cuda_stream)
         if rc != 0:
             raise RuntimeError(f"stream probe mode {mode}: error {rc}")
 
-    def rate(mode, nbytes, moved):
-        n = rotation(moved)
-        src = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(n)] \
-            if mode != 1 else [None] * n
-        dst = [torch.empty(nbytes if mode else 4096, dtype=torch.uint8, device=dev)
-               for _ in range(n)]
-        fns = [(lambda a=a, b=b: call(mode, a, b, nbytes)) for a, b in zip(src, dst)]
-        _, ev = time_graph(torch, fns, 20, 3, args.eager)
-        del src, dst, fns
-        return round(moved / ev / 1e9, 1)
+    n = rotation(moved)
+    src = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(n)] \
+        if mode != 1 else [None] * n
+    dst = [torch.empty(nbytes if mode else 4096, dtype=torch.uint8, device=dev)
+           for _ in range(n)]
+    fns = [(lambda a=a, b=b: call(a, b)) for a, b in zip(src, dst)]
+    _, ev = time_graph(torch, fns, 20, 3, args.eager)
+    del src, dst, fns
+    return round(moved / ev / 1e9, 1)
 
+
+def copy_probe_rate(torch, dev, args, moved):
+    """The copy probe over `moved` bytes of read + write (half each)."""
+    half = (moved // 2 + 15) // 16 * 16
+    return stream_probe_rate(torch, dev, args, 2, half, 2 * half)
+
+
+def stream_ceilings(torch, dev, args, store_bytes=None):
+    """GB/s that plain streaming kernels reach on this box: read-only,
+    write-only and copy over 512 MiB buffers, and a copy of the store's own
+    byte count (the prologue leg adds one of its own byte count).  These are the rates a read + write kernel (the store, the
+    prologue) and a read kernel (the decode) can be held against, besides the
+    8 TB/s peak."""
     big = 512 << 20
-    out = {"read_512mib_gbs": rate(0, big, big), "write_512mib_gbs": rate(1, big, big),
-           "copy_512mib_gbs": rate(2, big, 2 * big)}
+    out = {"read_512mib_gbs": stream_probe_rate(torch, dev, args, 0, big, big),
+           "write_512mib_gbs": stream_probe_rate(torch, dev, args, 1, big, big),
+           "copy_512mib_gbs": stream_probe_rate(torch, dev, args, 2, big, 2 * big)}
     if store_bytes:
-        half = (store_bytes // 2 + 15) // 16 * 16
-        out["copy_store_bytes_gbs"] = rate(2, half, 2 * half)
+        out["copy_store_bytes_gbs"] = copy_probe_rate(torch, dev, args, store_bytes)
     out["what"] = ("hand-written streaming kernels (16-byte non-temporal accesses, 4 per lane "
                    "in flight): GB/s of bytes read, written, or read + written (copy)")
     return out
@@ -926,6 +936,10 @@ def main():
             r = result["prologue"]["roofline"]
             r["frac_of_copy_probe"] = round(
                 r["achieved"] / result["stream_ceiling"]["copy_512mib_gbs"], 4)
+            log("timing the copy probe over the prologue's bytes")
+            same = copy_probe_rate(torch, dev, args, result["prologue"]["bytes_per_step"])
+            result["stream_ceiling"]["copy_prologue_bytes_gbs"] = same
+            r["frac_of_copy_probe_same_bytes"] = round(r["achieved"] / same, 4)
 
     # ------------------------------------------------------------------ prefill
     if "prefill" in legs:
