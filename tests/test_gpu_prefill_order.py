@@ -4,8 +4,9 @@ pairs by their key count and the attention kernel takes its tile from that
 order; without one the grid order is used.  The order only changes when a
 tile runs, so both calls must give the same bits, and the ordered one is also
 checked against the oracle (2e-2 abs / 1e-2 rel).  Cases: paged with cached
-prefixes (GQA groups 2, 4, 8; an empty sequence; one-token sequences),
-dense self-attention, and 300 short sequences (ties, empty sequences)."""
+prefixes (GQA groups 2, 4, 8; an empty sequence; one-token sequences; pages of
+16, 64, 128, 256 and 512 tokens), dense self-attention, and 300 short
+sequences (ties, empty sequences)."""
 import numpy as np
 import pytest
 import torch
@@ -34,6 +35,28 @@ def test_ordered_equals_grid_order_paged(hq, hkv):
     assert torch.equal(ordered, grid)
     ref = oracle_prefill_paged(q, kc, vc, bt, cu_q, cu_k, 256, 128 ** -0.5)
     assert_attn_close(ordered, ref, f"ordered paged prefill G={hq // hkv}")
+
+
+@pytest.mark.parametrize("bs", [16, 64, 128, 512])
+def test_ordered_equals_grid_order_block_sizes(bs):
+    """Pages of 64 / 128 / 512 tokens (the kernel's first page ids come from
+    shifts of another width) and of 16 tokens (tiles span pages: per-row
+    page lookups), each with the longest-first order in use."""
+    rng = np.random.default_rng(90 + bs)
+    lens_q = [int(x) for x in rng.integers(1, 700, 16)] + [0, 699]
+    lens_k = [q + int(c) for q, c in zip(lens_q, rng.integers(0, 800, len(lens_q)))]
+    q, kc, vc, bt, cu_q, cu_k = _paged_case(91 + bs, lens_q, lens_k, bs=bs)
+    args = (q.cuda(), kc.cuda(), vc.cuda(), cu_q.cuda(), cu_k.cuda(), max(lens_q), max(lens_k),
+            128 ** -0.5)
+    say(f"prefill order, {bs}-token pages: ordered")
+    ordered, ws = _call(*args, bt=bt.cuda(), use_ws=True)
+    pairs = len(lens_q) * ((max(lens_q) + 63) // 64)
+    assert pairs * 8 > 1024 and ws >= 4 * pairs   # the order is used
+    say(f"prefill order, {bs}-token pages: grid order")
+    grid, _ = _call(*args, bt=bt.cuda(), use_ws=False)
+    assert torch.equal(ordered, grid)
+    ref = oracle_prefill_paged(q, kc, vc, bt, cu_q, cu_k, bs, 128 ** -0.5)
+    assert_attn_close(ordered, ref, f"ordered paged prefill, {bs}-token pages")
 
 
 def test_ordered_equals_grid_order_dense():
