@@ -319,8 +319,11 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
 
   // LDS: K stages 0/1, then V stages 0/1 (64 KB).
   __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * kTileBytes];
-  auto k_stage = [&](int st) { return lds + st * kTileBytes; };
-  auto v_stage = [&](int st) { return lds + (2 + st) * kTileBytes; };
+  // LDS byte addresses of the stages, from one conversion of the array's
+  // address (converting each stage pointer would re-check it for null)
+  const uint32_t lds_base = lds_addr(lds);
+  auto k_stage = [&](int st) { return lds_base + (uint32_t)(st * kTileBytes); };
+  auto v_stage = [&](int st) { return lds_base + (uint32_t)((2 + st) * kTileBytes); };
 
   const int32_t* bt_row = MODE != kDense ? a.block_tables + (int64_t)s * a.bt_stride : nullptr;
 
@@ -387,11 +390,11 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
   // `page` / `in_page` (kPagedAligned): the tile's page id and its first key's
   // offset inside that page (multiples of 64, kept by the caller without
   // divisions).
-  auto plan_tile = [&](int kt, uint8_t* dst, bool is_v, int page, int in_page) {
+  auto plan_tile = [&](int kt, uint32_t dst, bool is_v, int page, int in_page) {
     DmaPlan pl;
     const int base = kt * kKeys;
     const uint16_t* src = is_v ? a.v : a.k;
-    pl.dst0 = uniform(lds_addr(dst + kTileRowsPerWave * wave * kRowBytes));
+    pl.dst0 = uniform(dst + (uint32_t)(kTileRowsPerWave * wave * kRowBytes));
     int rem = n_keys - base < kKeys ? n_keys - base : kKeys;
     rem = (rem > 0 && kt < t_end) ? rem : 0;
     if constexpr (MODE == kPagedAny) {
@@ -439,9 +442,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     t.bytes = ok ? (uint32_t)rem * k_row_bytes : 0u;
     return t;
   };
-  auto plan_at = [&](const TileOff& t, uint8_t* dst, bool is_v) {
+  auto plan_at = [&](const TileOff& t, uint32_t dst, bool is_v) {
     DmaPlan pl;
-    pl.dst0 = uniform(lds_addr(dst + kTileRowsPerWave * wave * kRowBytes));
+    pl.dst0 = uniform(dst + (uint32_t)(kTileRowsPerWave * wave * kRowBytes));
     const uint64_t b = (is_v ? head_v : head_k) + t.off;
     pl.rsrc = nvk_u32x4{uniform((uint32_t)b), uniform((uint32_t)(b >> 32) & 0xFFFFu),
                         uniform(t.bytes), 0x00020000u};
@@ -462,10 +465,10 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     }
   };
 
-  // Page ids (kPagedAligned): read one step before the tile's load is issued.
+  // Page ids (kPagedAligned): read one step before the tile's load is issued;
+  // `logical` is the tile's page index in the sequence, kept by the caller.
   const int last_page = n_keys > 0 ? (n_keys - 1) / a.block_size : 0;
-  auto fetch_page = [&](int kt) -> int {
-    int logical = a.bs_shift >= 0 ? (kt * kKeys) >> a.bs_shift : (kt * kKeys) / a.block_size;
+  auto fetch_page = [&](int logical) -> int {
     logical = logical < last_page ? logical : last_page;
     asm volatile("" : "+v"(logical));  // keep the table read a vector load
     return bt_row[logical];
@@ -486,7 +489,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
   // Lane reads key row 32 mb + l32, logical chunk 2 ks + half, i.e. byte
   // row*256 + 16*((2 ks + half) ^ swz(row)) = k_addr ^ (32 ks) (+ 8192 mb).
   const int k_swz = swz(l32);
-  const uint32_t k_addr0 = lds_addr(lds) + l32 * kRowBytes + 16 * ((half ^ k_swz) & 1) +
+  const uint32_t k_addr0 = lds_base + l32 * kRowBytes + 16 * ((half ^ k_swz) & 1) +
                            32 * (k_swz >> 1);
   // The XOR touches bits 5-7 only and the stage / block offsets are multiples
   // of 8 KiB, so the address of fragment ks in stage st, block mb is
@@ -524,7 +527,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     const int tr_key = (lane & 15) >> 2;                          // row within the 4-row group
     const int tr_c0 = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);  // chunk within 32 d
     const int sw_lo = swz(4 * half + tr_key), sw_hi = swz(8 + 4 * half + tr_key);
-    const uint32_t v0 = lds_addr(lds) + 2 * kTileBytes + 8 * (lane & 1);
+    const uint32_t v0 = lds_base + 2 * kTileBytes + 8 * (lane & 1);
     v_lo0 = v0 + (4 * half + tr_key) * kRowBytes + 16 * (tr_c0 ^ (sw_lo & 3)) + 64 * (sw_lo >> 2);
     v_hi0 = v0 + (8 + 4 * half + tr_key) * kRowBytes + 16 * (tr_c0 ^ (sw_hi & 3)) +
             64 * (sw_hi >> 2);
@@ -814,6 +817,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
                                            : plan_tile(tb + 2, k_stage(0), false, pg[2], ip[2]);
     int page_a = pg[2], page_b = pg[3];  // pages of tiles kt+2, kt+3
     int ip_a = ip[2], ip_b = ip[3];
+    // page index of tile kt+3 in the sequence (aligned paged mode), advanced
+    // with the in-page offsets instead of a division per step
+    int lp_b = MODE == kPagedAligned ? ((tb + 3) * kKeys) / a.block_size : 0;
     wait_lds_loads();
     __syncthreads();
     compute_s(std::integral_constant<int, 0>{}, sc);
@@ -838,10 +844,12 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       wait_lds_loads();
       __syncthreads();
       int page_c = 0;
+      const int ip_c = next_in_page(ip_b);               // tile kt+4
+      const int lp_c = ip_c == 0 ? lp_b + 1 : lp_b;
       if constexpr (MODE == kPagedAligned) {
         page_a = __builtin_amdgcn_readfirstlane(page_a);
         page_b = __builtin_amdgcn_readfirstlane(page_b);
-        if (kt + 4 < t_end) page_c = fetch_page(kt + 4);
+        if (kt + 4 < t_end) page_c = fetch_page(lp_c);
       }
       if constexpr (MODE == kPagedAny) {
         plan_v = plan_tile(kt + 1, v_stage(1 - P), true, 0, 0);
@@ -856,7 +864,8 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       page_a = page_b;
       page_b = page_c;
       ip_a = ip_b;
-      ip_b = next_in_page(ip_b);
+      ip_b = ip_c;
+      lp_b = lp_c;
     };
     int kt = tb;
     for (; kt + 1 < t_end; kt += 2) {
