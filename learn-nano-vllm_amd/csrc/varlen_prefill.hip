@@ -226,10 +226,10 @@ __device__ __forceinline__ QTile qtile_info(const PrefillArgs& a, int s, int qt,
   return t;
 }
 
-// Raw buffer descriptor over [base, base + bytes) (stride 0, dword3 0x00020000
-// = 32-bit data format, the gfx9 setting for untyped buffer access).
-__device__ __forceinline__ nvk_u32x4 tile_rsrc(const uint16_t* base, uint32_t bytes) {
-  const uint64_t b = (uint64_t)(uintptr_t)base;
+// Raw buffer descriptor over [b, b + bytes) for a byte address b (stride 0,
+// dword3 0x00020000 = 32-bit data format, the gfx9 setting for untyped buffer
+// access).
+__device__ __forceinline__ nvk_u32x4 tile_rsrc(uint64_t b, uint32_t bytes) {
   return nvk_u32x4{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, bytes, 0x00020000u};
 }
 
@@ -390,13 +390,27 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
   // `page` / `in_page` (kPagedAligned): the tile's page id and its first key's
   // offset inside that page (multiples of 64, kept by the caller without
   // divisions).
+  // Keys this workgroup loads: tiles past t_end and keys past n_keys get 0
+  // bytes, so a tile's byte count is one clamp of key_end - its first key.
+  const int key_end = n_keys < t_end * kKeys ? n_keys : t_end * kKeys;
+  auto tile_keys = [&](int kt) {
+    int rem = key_end - kt * kKeys;
+    rem = rem < kKeys ? rem : kKeys;
+    asm volatile("" : "+s"(rem));  // keeps the clamp scalar (as one op it is v_med3)
+    return rem > 0 ? rem : 0;
+  };
+  // Dense mode: the kv head's first element of this sequence's key rows; tile
+  // kt starts kt * 64 rows later.
+  const uint64_t dense_k = MODE == kDense ? (uint64_t)(uintptr_t)(a.k + (int64_t)k_row0 * a.k_stride_tok +
+                                                                  (int64_t)kvh * a.kv_stride_head) : 0;
+  const uint64_t dense_v = MODE == kDense ? (uint64_t)(uintptr_t)(a.v + (int64_t)k_row0 * a.v_stride_tok +
+                                                                  (int64_t)kvh * a.kv_stride_head) : 0;
   auto plan_tile = [&](int kt, uint32_t dst, bool is_v, int page, int in_page) {
     DmaPlan pl;
     const int base = kt * kKeys;
     const uint16_t* src = is_v ? a.v : a.k;
     pl.dst0 = uniform(dst + (uint32_t)(kTileRowsPerWave * wave * kRowBytes));
-    int rem = n_keys - base < kKeys ? n_keys - base : kKeys;
-    rem = (rem > 0 && kt < t_end) ? rem : 0;
+    const int rem = tile_keys(kt);
     if constexpr (MODE == kPagedAny) {
       pl.rsrc = nvk_u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
@@ -411,14 +425,12 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       uint32_t bytes = (uint32_t)rem * (is_v ? v_row_bytes : k_row_bytes);
       nvk_u32x4 r;
       if constexpr (MODE == kDense) {
-        const uint16_t* tb = src + (int64_t)(k_row0 + base) * (is_v ? a.v_stride_tok : a.k_stride_tok) +
-                             (int64_t)kvh * a.kv_stride_head;
-        r = tile_rsrc(tb, bytes);
+        const uint32_t row_bytes = is_v ? v_row_bytes : k_row_bytes;
+        r = tile_rsrc((is_v ? dense_v : dense_k) + (uint64_t)(uint32_t)base * row_bytes, bytes);
       } else {
         const bool ok = (uint32_t)page < (uint32_t)a.num_blocks;
         const uint64_t off = (uint64_t)(uint32_t)page * page_bytes + (uint32_t)in_page * k_row_bytes;
-        const uint64_t b = (is_v ? head_v : head_k) + (ok ? off : 0);  // no branch
-        r = nvk_u32x4{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, ok ? bytes : 0u, 0x00020000u};
+        r = tile_rsrc((is_v ? head_v : head_k) + (ok ? off : 0), ok ? bytes : 0u);  // no branch
       }
       pl.rsrc = nvk_u32x4{uniform(r.x), uniform(r.y), uniform(r.z), uniform(r.w)};
     }
@@ -433,21 +445,20 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     uint32_t bytes;
   };
   auto tile_off = [&](int kt, int page, int in_page) {
-    const int base = kt * kKeys;
-    int rem = n_keys - base < kKeys ? n_keys - base : kKeys;
-    rem = (rem > 0 && kt < t_end) ? rem : 0;
+    const int rem = tile_keys(kt);
     const bool ok = (uint32_t)page < (uint32_t)a.num_blocks;
+    // an invalid page loads nothing (0 bytes); its offset is then irrelevant
+    const uint32_t pg = ok ? (uint32_t)page : 0u;
     TileOff t;
-    t.off = ok ? (uint64_t)(uint32_t)page * page_bytes + (uint32_t)in_page * k_row_bytes : 0;
+    t.off = (uint64_t)pg * page_bytes + (uint32_t)in_page * k_row_bytes;
     t.bytes = ok ? (uint32_t)rem * k_row_bytes : 0u;
     return t;
   };
   auto plan_at = [&](const TileOff& t, uint32_t dst, bool is_v) {
     DmaPlan pl;
     pl.dst0 = uniform(dst + (uint32_t)(kTileRowsPerWave * wave * kRowBytes));
-    const uint64_t b = (is_v ? head_v : head_k) + t.off;
-    pl.rsrc = nvk_u32x4{uniform((uint32_t)b), uniform((uint32_t)(b >> 32) & 0xFFFFu),
-                        uniform(t.bytes), 0x00020000u};
+    const nvk_u32x4 r = tile_rsrc((is_v ? head_v : head_k) + t.off, t.bytes);
+    pl.rsrc = nvk_u32x4{uniform(r.x), uniform(r.y), uniform(r.z), r.w};
     return pl;
   };
   static_assert(4 * kRowBytes == 1024 && kLoadsPerWave <= 4, "load j lands at dst0 + j KiB");
