@@ -659,10 +659,13 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
   // Stages: tile t sits in stage (t - t_begin) & 1, so the step loop runs
   // two steps per pass and every stage offset is a constant (P: the stage of
   // tile kt).
-  auto mma_step = [&](auto par, int kt, nvk_f32x16 (&sc)[2], float moff, const DmaPlan& plan_v,
-                      const DmaPlan& plan_k, int pg_v, int ip_v, int pg_k, int ip_k,
-                      DmaPlan& next_v, DmaPlan& next_k, float& mt_next, TileOff& toff) {
+  // LAST: the step of the range's last tile, which has no S(kt+1), row max or
+  // loads of its own to make.
+  auto mma_step = [&](auto par, auto last, int kt, nvk_f32x16 (&sc)[2], float moff,
+                      const DmaPlan& plan_v, const DmaPlan& plan_k, int pg_v, int ip_v, int pg_k,
+                      int ip_k, DmaPlan& next_v, DmaPlan& next_k, float& mt_next, TileOff& toff) {
     constexpr int P = decltype(par)::value;
+    constexpr bool LAST = decltype(last)::value;
     auto rd_k = [&](int ks, int mb) {  // K of tile kt+1
       return *reinterpret_cast<const __attribute__((address_space(3))) vec8*>(
           (size_t)(k_addr[ks] + (1 - P) * kTileBytes + 32 * kRowBytes * mb));
@@ -716,7 +719,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       __builtin_amdgcn_sched_barrier(0);
       acc_o[db] = E::mfma32x32x16(vf[idx % 3], pf[ks], acc_o[db]);
       const int j = v_load_at(idx);
-      if (j >= 0) issue_load(plan_v, j, true);
+      if (j >= 0 && !LAST) issue_load(plan_v, j, true);
     };
     // O k-step 0 with fragment 1 (words 4-7; word 8 started).
 #pragma unroll
@@ -727,19 +730,22 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       __builtin_amdgcn_sched_barrier(0);
     }
     pf[1] = pack(pw);
-    // S(kt+1), block 0 then block 1.  After the last tile this multiplies a
-    // stale (or zero-filled) K stage; the result is unused.
+    // S(kt+1), block 0 then block 1 (LAST: only the exp2 of fragments 2-3).
     vec8 kf[3];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      kf[0] = rd_k(0, mb);
-      kf[1] = rd_k(1, mb);
-      sc[mb] = nvk_f32x16{};
+    for (int mb = 0; mb < (LAST ? 1 : 2); ++mb) {
+      if constexpr (!LAST) {
+        kf[0] = rd_k(0, mb);
+        kf[1] = rd_k(1, mb);
+        sc[mb] = nvk_f32x16{};
+      }
 #pragma unroll
       for (int ks = 0; ks < HD / 16; ++ks) {
-        if (ks + 2 < HD / 16) kf[(ks + 2) % 3] = rd_k(ks + 2, mb);
-        __builtin_amdgcn_sched_barrier(0);
-        sc[mb] = E::mfma32x32x16(kf[ks % 3], qf[ks], sc[mb]);
+        if constexpr (!LAST) {
+          if (ks + 2 < HD / 16) kf[(ks + 2) % 3] = rd_k(ks + 2, mb);
+          __builtin_amdgcn_sched_barrier(0);
+          sc[mb] = E::mfma32x32x16(kf[ks % 3], qf[ks], sc[mb]);
+        }
         if (mb == 0) {  // fragments 2-3: words 8-15
           const uint32_t w = exp_finish(xp[ks & 1], 8 + ks);
           if (ks < 4) pw[ks] = w;
@@ -747,8 +753,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
           if (ks < 7) xp[(9 + ks) & 1] = exp_start(sc, moff, 9 + ks);
         }
         const int j = k_load_at(8 * mb + ks);
-        if (j >= 0) issue_load(plan_k, j, false);
-        if constexpr (MODE == kPagedAligned) {  // toff: tile kt+2 in, tile kt+3 out
+        if (j >= 0 && !LAST) issue_load(plan_k, j, false);
+        if constexpr (LAST) {
+        } else if constexpr (MODE == kPagedAligned) {  // toff: tile kt+2 in, tile kt+3 out
           if (mb == 0 && ks == 5) next_v = plan_at(toff, v_stage(P), true);
           if (mb == 1 && ks == 1) {
             toff = tile_off(kt + 3, pg_k, ip_k);
@@ -766,7 +773,7 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
         pf[3] = pack(pw3);
       }
     }
-    mask_tile(sc, kt + 1);
+    if constexpr (!LAST) mask_tile(sc, kt + 1);
     // O k-steps 1-3 with the row max of S(kt+1): chains 0-1 (score block 0)
     // beside MFMAs 4-6, chains 2-3 (block 1, just computed) beside 8-10, the
     // join beside 11-12.
@@ -774,16 +781,18 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
 #pragma unroll
     for (int idx = 4; idx < kO; ++idx) {
       o_mfma(idx);
-      if (idx >= 4 && idx < 7) {
-        ch[0] = max_chain(sc, ch[0], 0, idx - 4);
-        ch[1] = max_chain(sc, ch[1], 1, idx - 4);
+      if constexpr (!LAST) {
+        if (idx >= 4 && idx < 7) {
+          ch[0] = max_chain(sc, ch[0], 0, idx - 4);
+          ch[1] = max_chain(sc, ch[1], 1, idx - 4);
+        }
+        if (idx >= 8 && idx < 11) {
+          ch[2] = max_chain(sc, ch[2], 2, idx - 8);
+          ch[3] = max_chain(sc, ch[3], 3, idx - 8);
+        }
+        if (idx == 11) max_join_a(sc, ch, tj);
+        if (idx == 12) mt_next = max_join_b(sc, tj);
       }
-      if (idx >= 8 && idx < 11) {
-        ch[2] = max_chain(sc, ch[2], 2, idx - 8);
-        ch[3] = max_chain(sc, ch[3], 3, idx - 8);
-      }
-      if (idx == 11) max_join_a(sc, ch, tj);
-      if (idx == 12) mt_next = max_join_b(sc, tj);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -850,8 +859,9 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     // changes nothing and is skipped.  A row that sees no key of the tile
     // keeps -inf.
     m_ref = mt;
-    auto step = [&](auto par, int kt) {
+    auto step = [&](auto par, auto last, int kt) {
       constexpr int P = decltype(par)::value;
+      constexpr bool LAST = decltype(last)::value;
       wait_lds_loads();
       __syncthreads();
       int page_c = 0;
@@ -862,14 +872,14 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
         page_b = __builtin_amdgcn_readfirstlane(page_b);
         if (kt + 4 < t_end) page_c = fetch_page(lp_c);
       }
-      if constexpr (MODE == kPagedAny) {
+      if constexpr (MODE == kPagedAny && !LAST) {
         plan_v = plan_tile(kt + 1, v_stage(1 - P), true, 0, 0);
         plan_k = plan_tile(kt + 2, k_stage(P), false, 0, 0);
       }
       const float moff = rescale(mt);
       DmaPlan next_v = plan_v, next_k = plan_k;
-      mma_step(par, kt, sc, moff, plan_v, plan_k, page_a, ip_a, page_b, ip_b, next_v, next_k, mt,
-               toff);
+      mma_step(par, last, kt, sc, moff, plan_v, plan_k, page_a, ip_a, page_b, ip_b, next_v, next_k,
+               mt, toff);
       plan_v = next_v;
       plan_k = next_k;
       page_a = page_b;
@@ -878,12 +888,21 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
       ip_b = ip_c;
       lp_b = lp_c;
     };
+    const std::integral_constant<int, 0> p0;
+    const std::integral_constant<int, 1> p1;
+    const std::false_type more;
+    const std::true_type last;
     int kt = tb;
-    for (; kt + 1 < t_end; kt += 2) {
-      step(std::integral_constant<int, 0>{}, kt);
-      step(std::integral_constant<int, 1>{}, kt + 1);
+    for (; kt + 2 < t_end; kt += 2) {
+      step(p0, more, kt);
+      step(p1, more, kt + 1);
     }
-    if (kt < t_end) step(std::integral_constant<int, 0>{}, kt);
+    if (kt + 1 < t_end) {  // two tiles left
+      step(p0, more, kt);
+      step(p1, last, kt + 1);
+    } else {
+      step(p0, last, kt);
+    }
   }
 
   // ---- epilogue: normalise and store the row -----------------------------------
