@@ -754,14 +754,13 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
         }
         const int j = k_load_at(8 * mb + ks);
         if (j >= 0 && !LAST) issue_load(plan_k, j, false);
-        if constexpr (LAST) {
-        } else if constexpr (MODE == kPagedAligned) {  // toff: tile kt+2 in, tile kt+3 out
+        if constexpr (!LAST && MODE == kPagedAligned) {  // toff: tile kt+2 in, tile kt+3 out
           if (mb == 0 && ks == 5) next_v = plan_at(toff, v_stage(P), true);
           if (mb == 1 && ks == 1) {
             toff = tile_off(kt + 3, pg_k, ip_k);
             next_k = plan_at(toff, k_stage(1 - P), false);
           }
-        } else if constexpr (MODE == kDense) {
+        } else if constexpr (!LAST && MODE == kDense) {
           if (mb == 0 && ks == 5) next_v = plan_tile(kt + 2, v_stage(P), true, pg_v, ip_v);
           if (mb == 1 && ks == 1)
             next_k = plan_tile(kt + 3, k_stage(1 - P), false, pg_k, ip_k);
