@@ -451,16 +451,20 @@ int nvk_gather_last_tokens(const void* x, int64_t x_row_stride, const int32_t* c
 /*
  * Temperature sampling (nanovllm/layers/sampler.py:7-12):
  *   tokens[b] = argmax_i softmax(logits[b] / temperatures[b])_i / max(E_i, 1e-10)
- * with E_i ~ Exp(1), evaluated as argmax_i logits[b][i] / T - log max(E_i, 1e-10)
- * (the same maximiser: the softmax normaliser is one constant per row).
- * noise != NULL: E = noise[b][i] (float32, row stride noise_row_stride);
- * noise == NULL: E = -ln(u), u in (0, 1] from Philox4x32-10 keyed by seed,
- * counter (offset + i/4, b): advance offset by at least ceil(vocab/4) between
- * calls that must draw independently.  Ties go to the smallest index.
+ * with E_i ~ Exp(1): token i is drawn with probability softmax(logits[b] / T)_i.
+ * noise != NULL: E = noise[b][i] (float32, row stride noise_row_stride), and
+ * the argmax is evaluated as argmax_i logits[b][i] / T - log max(E_i, 1e-10)
+ * (the same maximiser: the softmax normaliser is one constant per row); ties
+ * go to the smallest index.
+ * noise == NULL: the same distribution drawn by inverse transform with
+ * uniforms from Philox4x32-10 keyed by seed at counters (offset, b, w) for
+ * w < 2 + ceil(vocab / 2048): calls that must draw independently use
+ * different offsets.  Non-finite logits carry no mass.
+ * Rows without a finite logit give token 0.
  * logits: bf16 or f32 [batch][row_stride]; tokens: int64 [batch].
- * workspace: nvk_sample_workspace_size() bytes (16-byte aligned; per row and
- * 8192-element chunk one (score, index) winner), need not be initialised.
- * Two kernels: per-chunk winners, then one wave per row.
+ * workspace: nvk_sample_workspace_size() bytes (16-byte aligned; three 4-byte
+ * slots per row and 2048 logits), need not be initialised.
+ * Two kernels: one workgroup per row and 8192 logits, then one wave per row.
  */
 size_t nvk_sample_workspace_size(int32_t batch, int32_t vocab);
 int nvk_sample(const void* logits, int64_t row_stride, int32_t batch, int32_t vocab,

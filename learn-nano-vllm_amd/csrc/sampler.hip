@@ -8,55 +8,33 @@
 // Sampler (nanovllm/layers/sampler.py:7-12):
 //   probs = softmax(logits.float() / temperature[b]);
 //   token = argmax_i probs_i / max(E_i, 1e-10),  E_i ~ Exp(1) i.i.d.
-// This is the exponential race: the winner is distributed as probs.  The
-// softmax normaliser is one positive constant per row and exp is monotone, so
-//   argmax_i probs_i / E_i = argmax_i (logits_i / T - log E_i),
-// which needs no max or sum pass: one read of the logits row.  The noise is
-// either the caller's (E, float32 [B][V]: used as given, for reproducing a
-// reference draw) or drawn in the kernel from Philox4x32-10 (Salmon, Moraes,
-// Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3", SC'11) keyed by
-// (seed) and counted by (offset, row, element / 4), E = -log(u) with u in
-// (0, 1].  Ties go to the smallest index.
-//
-// Work split: a row is cut into chunks of 8192 elements, one 256-thread
-// workgroup each (8 elements per thread per pass, 4 passes), so even a
-// 64-row step fills the GPU; each workgroup leaves its (score, index) winner
-// in the workspace and a second kernel (one wave per row) picks the row's
-// winner.  The Philox draw (quarter-rate 32x32->64 multiplies) and the two
-// log2 per element, not the logits read, bound the kernel.  So for large
-// steps (batch x vocab >= 2^24) without the caller's noise, the draw is an
-// inverse-CDF one instead (two uniforms per row; see sample_mass_kernel).
+// This is the exponential race: the winner is distributed as probs.
+// * With the caller's noise (E, float32 [B][V]: used as given, for
+//   reproducing a reference draw) the race itself is evaluated: the softmax
+//   normaliser is one positive constant per row and exp is monotone, so
+//     argmax_i probs_i / E_i = argmax_i (logits_i / T - log E_i),
+//   which needs no max or sum pass: one read of the logits and the noise.
+//   Ties go to the smallest index.  A row is cut into chunks of 8192
+//   elements, one 256-thread workgroup each (8 elements per thread per pass,
+//   4 passes), so even a 64-row step fills the GPU; each workgroup leaves its
+//   (score, index) winner in the workspace and a second kernel (one wave per
+//   row) picks the row's winner.
+// * Without it the kernel draws from the same distribution by inverse
+//   transform (sample_draw_kernel): uniforms from Philox4x32-10 (Salmon,
+//   Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3", SC'11)
+//   keyed by (seed), two per 2048 logits and one per row, instead of one
+//   exponential per element (whose Philox draw and logarithms, not the
+//   logits read, bounded the race).
 #include "nvk_common.h"
 
 namespace {
 
 constexpr float kMinNoise = 1e-10f;  // clamp_min_(1e-10), sampler.py:11
 
-// ---- Philox4x32-10 (constants from the SC'11 paper) -------------------------
+// Philox4x32-10 counter and output block (the rounds: row_uniforms)
 struct U4 {
   uint32_t x, y, z, w;
 };
-
-// hi(p1) ^ c.y ^ k0 and hi(p0) ^ c.w ^ k1 as one three-input v_bitop3_b32 each
-// (truth table 0x96 = a ^ b ^ c); the 32x32->64 products are v_mad_u64_u32.
-__device__ __forceinline__ U4 philox_round(U4 c, uint32_t k0, uint32_t k1) {
-  const uint64_t p0 = (uint64_t)0xD2511F53u * c.x;
-  const uint64_t p1 = (uint64_t)0xCD9E8D57u * c.z;
-  return U4{(uint32_t)__builtin_amdgcn_bitop3_b32((uint32_t)(p1 >> 32), c.y, k0, 0x96),
-            (uint32_t)p1,
-            (uint32_t)__builtin_amdgcn_bitop3_b32((uint32_t)(p0 >> 32), c.w, k1, 0x96),
-            (uint32_t)p0};
-}
-
-__device__ __forceinline__ U4 philox10(U4 c, uint32_t k0, uint32_t k1) {
-#pragma unroll
-  for (int r = 0; r < 10; ++r) {
-    c = philox_round(c, k0, k1);
-    k0 += 0x9E3779B9u;
-    k1 += 0xBB67AE85u;
-  }
-  return c;
-}
 
 struct SampleArgs {
   const void* logits;
@@ -64,15 +42,15 @@ struct SampleArgs {
   int vocab, chunks;
   int vec_ok;  // bf16 rows 16-byte aligned: 16-byte loads
   const float* temperatures;
-  const float* noise;  // null: Philox
+  const float* noise;  // null: the kernel's own draw (Philox)
   int64_t noise_stride;
   uint64_t seed, offset;
-  float* part_score;  // [batch][chunks]
-  int* part_index;
+  float* part_score;  // [batch][chunks]: the race's best score, or M_c
+  int* part_index;    // [batch][chunks]: the race's best index, or S_c (float bits)
+  int* part_token;    // [batch][chunks]: the chunk's drawn token (inverse CDF)
   int64_t* tokens;
 };
 
-constexpr int64_t kCdfMinElements = int64_t{1} << 24;  // batch x vocab for the inverse-CDF path
 constexpr int kPartThreads = 256;
 constexpr int kIters = 4;
 constexpr int kChunk = kPartThreads * 8 * kIters;  // elements of a row per workgroup
@@ -106,70 +84,37 @@ __device__ __forceinline__ void load8(const SampleArgs& a, int row, int base, bo
   }
 }
 
-// log2 of the exponential noise E of elements base .. base+7 of a row: from
-// the caller's draw e[0..7] (NOISE), or from Philox at counter (offset +
-// base/4 + h, row) for h = 0, 1.
-template <bool NOISE>
-__device__ __forceinline__ void noise_log2(const SampleArgs& a, int row, int base, const float* e,
-                                           float* le) {
-  if constexpr (NOISE) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) le[i] = __builtin_amdgcn_logf(fmaxf(e[i], kMinNoise));
-  } else {
-    const uint32_t k0 = (uint32_t)a.seed, k1 = (uint32_t)(a.seed >> 32);
-    const uint64_t ctr = a.offset + (uint64_t)(base >> 2);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const U4 r = philox10(U4{(uint32_t)(ctr + h), (uint32_t)((ctr + h) >> 32), (uint32_t)row, 0u},
-                            k0, k1);
-      const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        // u = (bits + 1) 2^-32 in (0, 1]; E / ln 2 = -log2(u), clamped like E >= 1e-10
-        const float u = ((float)w[j] + 1.0f) * 2.3283064365386963e-10f;
-        const float e2 = fmaxf(-__builtin_amdgcn_logf(u), kMinNoise * 1.4426950408889634f);
-        le[4 * h + j] = __builtin_amdgcn_logf(e2);
-      }
-    }
-  }
-}
-
-// Scores of one row chunk in log2 units: logits * log2(e) / T - log2(E)
-// (the base change and the constant log2(ln 2) of E = -ln u = -log2(u) ln 2
-// are common to every element of the row and do not move the maximiser).
-template <typename T, bool NOISE>
+// Race scores of one row chunk in log2 units: logits * log2(e) / T - log2(E),
+// E = max(noise, 1e-10) (the base change does not move the maximiser).
+template <typename T>
 __global__ __launch_bounds__(kPartThreads) void sample_partial_kernel(SampleArgs a) {
   const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
   const float scale = NVK_LOG2E / a.temperatures[row];
   float best = -INFINITY;
   int best_i = 0x7fffffff;
   if (sizeof(T) == 2 && a.vec_ok && (int64_t)(c + 1) * kChunk <= a.vocab) {
-    // a whole chunk of bf16: its logits (and the caller's noise) are all
-    // loaded before the first wait, so the loads overlap the Philox draw
+    // a whole chunk of bf16: its logits and noise are all loaded before the
+    // first wait
     const int64_t off = (int64_t)c * kChunk + tid * 8;
     const uint16_t* p = static_cast<const uint16_t*>(a.logits) + (int64_t)row * a.row_stride + off;
     nvk_u32x4 w[kIters];
 #pragma unroll
     for (int it = 0; it < kIters; ++it)
       w[it] = *reinterpret_cast<const nvk_u32x4*>(p + it * kPartThreads * 8);
-    float nz[NOISE ? kIters : 1][8];
-    if constexpr (NOISE) {
-      const float* q = a.noise + (int64_t)row * a.noise_stride + off;
+    float nz[kIters][8];
+    const float* q = a.noise + (int64_t)row * a.noise_stride + off;
 #pragma unroll
-      for (int it = 0; it < kIters; ++it)
+    for (int it = 0; it < kIters; ++it)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) nz[it][i] = q[it * kPartThreads * 8 + i];
-    }
+      for (int i = 0; i < 8; ++i) nz[it][i] = q[it * kPartThreads * 8 + i];
 #pragma unroll
     for (int it = 0; it < kIters; ++it) {
       const int base = c * kChunk + (it * kPartThreads + tid) * 8;
-      float le[8];
-      noise_log2<NOISE>(a, row, base, nz[NOISE ? it : 0], le);
       const uint32_t ww[4] = {w[it].x, w[it].y, w[it].z, w[it].w};
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float l = (i & 1) ? nvk_bf16hi_to_f32(ww[i >> 1]) : nvk_bf16lo_to_f32(ww[i >> 1]);
-        const float sc = l * scale - le[i];
+        const float sc = l * scale - __builtin_amdgcn_logf(fmaxf(nz[it][i], kMinNoise));
         // a thread visits its indices in increasing order: strictly greater wins
         if (sc > best) {
           best = sc;
@@ -185,17 +130,11 @@ __global__ __launch_bounds__(kPartThreads) void sample_partial_kernel(SampleArgs
       const bool full = base + 8 <= a.vocab;
       float l[8];
       load8<T>(a, row, base, full, l);
-      float e[8];
-      if constexpr (NOISE) {
-        const float* q = a.noise + (int64_t)row * a.noise_stride + base;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) e[i] = (full || base + i < a.vocab) ? q[i] : 1.0f;
-      }
-      float le[8];
-      noise_log2<NOISE>(a, row, base, e, le);
+      const float* q = a.noise + (int64_t)row * a.noise_stride + base;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float sc = l[i] * scale - le[i];
+        const float e = (full || base + i < a.vocab) ? q[i] : 1.0f;
+        const float sc = l[i] * scale - __builtin_amdgcn_logf(fmaxf(e, kMinNoise));
         // a thread visits its indices in increasing order: strictly greater wins
         if (sc > best && (full || base + i < a.vocab)) {
           best = sc;
@@ -261,16 +200,24 @@ __global__ __launch_bounds__(256) void sample_final_kernel(SampleArgs a, int bat
 
 // ---- the kernel's own randomness: inverse-CDF sampling ----------------------
 // Without the caller's noise the token is drawn by inverse transform over the
-// row's softmax, with two uniforms per row instead of one exponential per
-// element (the Philox draw per element, not the logits read, bounded the
-// race): the mass kernel reduces every chunk of the row to its maximum M_c of
-// x_i = logits_i * log2(e) / T and S_c = sum_i 2^(x_i - M_c); the pick kernel
-// draws (u1, u2) from Philox4x32-10 keyed by (seed) at counter (offset, row),
-// selects chunk c with probability S_c 2^(M_c - M) / sum, then the first index
-// of that chunk whose running sum of 2^(x_i - M_c) reaches u2 S_c.  A token is
-// drawn with probability p_i up to float32 rounding of the running sums (a
-// token with less than ~2^-24 of its chunk's mass is not drawn).  Rows with no
-// finite score give token 0, as in the race.
+// row's softmax instead of by the race (whose Philox draw per element, not the
+// logits read, bounds it).  One read of the logits.  The draw kernel cuts a
+// row into wave chunks of 2048 elements (each wave of a 256-thread workgroup
+// takes every fourth run of 512 elements of the workgroup's 8192); a wave
+// reduces its chunk to the maximum M_w of x_i = logits_i * log2(e) / T and
+// S_w = sum_i 2^(x_i - M_w), and draws the chunk's own token in two steps
+// with two uniforms (u1, u2) from Philox4x32-10 at counter (offset, row,
+// 2 + wave chunk): the lane whose running share of S_w first reaches u1 S_w,
+// then the first of that lane's 32 elements whose running sum reaches u2 times
+// the lane's sum.  The choose kernel draws u from Philox at (offset, row, 1),
+// selects wave chunk w with probability S_w 2^(M_w - M) / sum and returns its
+// token.  Each step's choice is independent of the others and proportional to
+// the mass it selects, so token i is drawn with probability
+//   S_w 2^(M_w - M) / sum * s_lane / S_w * 2^(x_i - M_w) / s_lane = p_i
+// up to float32 rounding of the running sums (a token with less than ~2^-24
+// of its lane's mass is not drawn).  Which order the sums walk does not change
+// the distribution.  Non-finite logits carry no mass; rows with no finite
+// score give token 0, as in the race.
 
 // x of one element (non-finite logits: -inf, no mass)
 __device__ __forceinline__ float mass_x(float l, float scale) {
@@ -278,55 +225,76 @@ __device__ __forceinline__ float mass_x(float l, float scale) {
   return (x == x && x != INFINITY) ? x : -INFINITY;
 }
 
-__device__ __forceinline__ float block_max256(float v, float* red) {
+__device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-  const int tid = threadIdx.x;
-  __syncthreads();
-  if ((tid & 63) == 0) red[tid >> 6] = v;
-  __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  return v;
 }
-__device__ __forceinline__ float block_sum256(float v, float* red) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-  const int tid = threadIdx.x;
-  __syncthreads();
-  if ((tid & 63) == 0) red[tid >> 6] = v;
-  __syncthreads();
-  return (red[0] + red[1]) + (red[2] + red[3]);
-}
-// Exclusive prefix of v over the 256 threads (in thread order); *total = sum.
-__device__ __forceinline__ float block_excl256(float v, float* red, float* total) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  float x = v;
+// Inclusive prefix of v over the 64 lanes of a wave (in lane order).
+__device__ __forceinline__ float wave_incl(float v) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const float y = __shfl_up(x, o);
-    if (lane >= o) x += y;
+    const float y = __shfl_up(v, o);
+    if (lane >= o) v += y;
   }
-  __syncthreads();
-  if (lane == 63) red[w] = x;
-  __syncthreads();
-  float before = 0.f;
-  for (int i = 0; i < w; ++i) before += red[i];
-  *total = (red[0] + red[1]) + (red[2] + red[3]);
-  return before + x - v;
+  return v;
+}
+
+// two uniforms in (0, 1] from Philox4x32-10 at counter (offset, row, word),
+// for a counter the same in every lane: plain xors, so that the rounds run on
+// the scalar unit (v_bitop3_b32 has no scalar form)
+__device__ __forceinline__ void row_uniforms(const SampleArgs& a, uint32_t row, uint32_t word,
+                                             float* u1, float* u2) {
+  U4 r{(uint32_t)a.offset, (uint32_t)(a.offset >> 32), row, word};
+  uint32_t k0 = (uint32_t)a.seed, k1 = (uint32_t)(a.seed >> 32);
+#pragma unroll
+  for (int i = 0; i < 10; ++i) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * r.x;
+    const uint64_t p1 = (uint64_t)0xCD9E8D57u * r.z;
+    r = U4{(uint32_t)(p1 >> 32) ^ r.y ^ k0, (uint32_t)p1, (uint32_t)(p0 >> 32) ^ r.w ^ k1,
+           (uint32_t)p0};
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  *u1 = ((float)r.x + 1.0f) * 2.3283064365386963e-10f;
+  *u2 = ((float)r.y + 1.0f) * 2.3283064365386963e-10f;
+}
+
+// Index of the first of cum[0..31] (non-decreasing) that reaches t, for
+// 0 < t <= cum[31]: five halvings, each a compare and selects.
+__device__ __forceinline__ int first_reaching(const float (&cum)[32], float t) {
+  float h16[16], h8[8], h4[4], h2[2];
+  bool b = cum[15] < t;
+  int idx = b ? 16 : 0;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) h16[j] = b ? cum[16 + j] : cum[j];
+  b = h16[7] < t;
+  idx += b ? 8 : 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) h8[j] = b ? h16[8 + j] : h16[j];
+  b = h8[3] < t;
+  idx += b ? 4 : 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) h4[j] = b ? h8[4 + j] : h8[j];
+  b = h4[1] < t;
+  idx += b ? 2 : 0;
+  h2[0] = b ? h4[2] : h4[0];
+  h2[1] = b ? h4[3] : h4[1];
+  return idx + (h2[0] < t ? 1 : 0);
 }
 
 template <typename T>
-__global__ __launch_bounds__(kPartThreads) void sample_mass_kernel(SampleArgs a) {
-  static_assert(kPartThreads == 256, "block reductions assume 256 threads");
-  const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
-  __shared__ float red[4];
+__global__ __launch_bounds__(kPartThreads) void sample_draw_kernel(SampleArgs a) {
+  const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const float scale = NVK_LOG2E / a.temperatures[row];
-  float x[kIters][8];
-  float mx = -INFINITY;
+  // element k = 8 it + i of the lane: c kChunk + (it kPartThreads + tid) 8 + i
+  float l[32];
+  const int first = c * kChunk + tid * 8;
   if (sizeof(T) == 2 && a.vec_ok && (int64_t)(c + 1) * kChunk <= a.vocab) {
-    // a whole chunk of bf16: the kIters 16-byte loads all leave before the
-    // first wait (the loop below waits for each in turn)
-    const uint16_t* p = static_cast<const uint16_t*>(a.logits) + (int64_t)row * a.row_stride +
-                        c * kChunk + tid * 8;
+    // a whole chunk of bf16: the kIters 16-byte loads all leave before the first wait
+    const uint16_t* p = static_cast<const uint16_t*>(a.logits) + (int64_t)row * a.row_stride + first;
     nvk_u32x4 w[kIters];
 #pragma unroll
     for (int it = 0; it < kIters; ++it)
@@ -336,163 +304,139 @@ __global__ __launch_bounds__(kPartThreads) void sample_mass_kernel(SampleArgs a)
       const uint32_t ww[4] = {w[it].x, w[it].y, w[it].z, w[it].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        x[it][2 * i] = mass_x(nvk_bf16lo_to_f32(ww[i]), scale);
-        x[it][2 * i + 1] = mass_x(nvk_bf16hi_to_f32(ww[i]), scale);
-        mx = fmaxf(mx, fmaxf(x[it][2 * i], x[it][2 * i + 1]));
+        l[8 * it + 2 * i] = nvk_bf16lo_to_f32(ww[i]);
+        l[8 * it + 2 * i + 1] = nvk_bf16hi_to_f32(ww[i]);
       }
     }
   } else {
 #pragma unroll
     for (int it = 0; it < kIters; ++it) {
-      const int base = c * kChunk + (it * kPartThreads + tid) * 8;
-      float l[8];
+      const int base = first + it * kPartThreads * 8;
       if (base < a.vocab) {
-        load8<T>(a, row, base, base + 8 <= a.vocab, l);
+        load8<T>(a, row, base, base + 8 <= a.vocab, &l[8 * it]);
       } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) l[i] = -INFINITY;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        x[it][i] = mass_x(l[i], scale);
-        mx = fmaxf(mx, x[it][i]);
+        for (int i = 0; i < 8; ++i) l[8 * it + i] = -INFINITY;
       }
     }
   }
-  const float M = block_max256(mx, red);
-  float sum = 0.f;
-  if (M != -INFINITY) {
+  // The wave's maximum and running sums, from the raw logits (the scale is
+  // positive).  A NaN logit leaves a NaN sum and a +inf one an infinite
+  // maximum: then the wave takes the path that gives them no mass.
+  float mx = l[0];
 #pragma unroll
-    for (int it = 0; it < kIters; ++it)
+  for (int k = 1; k < 32; k += 2) mx = fmaxf(mx, fmaxf(l[k], k + 1 < 32 ? l[k + 1] : l[k]));
+  float M = wave_max(mx) * scale;
+  float cum[32];
+  float run = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sum += exp2f(x[it][i] - M);
+  for (int k = 0; k < 32; ++k) {
+    run += __builtin_amdgcn_exp2f(fmaf(l[k], scale, -M));
+    cum[k] = run;
   }
-  const float S = block_sum256(sum, red);
-  if (tid == 0) {
-    a.part_score[(int64_t)row * a.chunks + c] = M;
-    reinterpret_cast<float*>(a.part_index)[(int64_t)row * a.chunks + c] = S;
+  if (__builtin_amdgcn_readfirstlane(__ballot(!(run == run)) != 0) ||
+      !(M > -INFINITY && M < INFINITY)) {
+#pragma unroll
+    for (int k = 0; k < 32; ++k) l[k] = mass_x(l[k], scale);
+    mx = l[0];
+#pragma unroll
+    for (int k = 1; k < 32; ++k) mx = fmaxf(mx, l[k]);
+    M = wave_max(mx);
+    run = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      run += M != -INFINITY ? __builtin_amdgcn_exp2f(l[k] - M) : 0.f;
+      cum[k] = run;
+    }
+  }
+  // the lane, then the element of the lane
+  const float incl = wave_incl(run);
+  const float total = __shfl(incl, 63);
+  float u1, u2;
+  row_uniforms(a, (uint32_t)row, 2u + (uint32_t)(c * (kPartThreads / 64) + wave), &u1, &u2);
+  const uint64_t pos = __ballot(run > 0.f);
+  const uint64_t hit = __ballot(run > 0.f && incl >= u1 * total);
+  // rounding can leave every running share below the target: the last lane with mass
+  const int pick = hit ? __builtin_ctzll(hit) : (pos ? 63 - __builtin_clzll(pos) : 0);
+  const int k = first_reaching(cum, fmaxf(u2 * run, 1.401298464e-45f));
+  const int tok = first + (k >> 3) * (kPartThreads * 8) + (k & 7);
+  const int tok_pick = __shfl(tok, pick);
+  if (lane == 0) {
+    const int64_t slot = (int64_t)row * (a.chunks * (kPartThreads / 64)) + c * (kPartThreads / 64) + wave;
+    a.part_score[slot] = pos ? M : -INFINITY;
+    reinterpret_cast<float*>(a.part_index)[slot] = total;
+    a.part_token[slot] = pos ? tok_pick : -1;
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(256) void sample_pick_kernel(SampleArgs a) {
-  const int row = blockIdx.x, tid = threadIdx.x;
-  __shared__ float red[4];
-  const float* pm = a.part_score + (int64_t)row * a.chunks;
-  const float* ps = reinterpret_cast<const float*>(a.part_index) + (int64_t)row * a.chunks;
-  float m = -INFINITY;
-  for (int c = tid; c < a.chunks; c += 256) m = fmaxf(m, pm[c]);
-  const float Mg = block_max256(m, red);
-  if (Mg == -INFINITY) {  // no finite score in the row
-    if (tid == 0) a.tokens[row] = 0;
+// One wave per row: wave chunk w with probability S_w 2^(M_w - M) / sum, then
+// its drawn token.
+__global__ __launch_bounds__(256) void sample_choose_kernel(SampleArgs a, int batch) {
+  constexpr int kCached = 2;  // entries per lane held in registers (rows of up to 128 wave chunks)
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= batch) return;
+  const int n = a.chunks * (kPartThreads / 64);
+  const int64_t r0 = (int64_t)row * n;
+  const float* pm = a.part_score + r0;
+  const float* ps = reinterpret_cast<const float*>(a.part_index) + r0;
+  const int* pt = a.part_token + r0;
+  float m[kCached], sm[kCached];
+  int tk[kCached];
+#pragma unroll
+  for (int j = 0; j < kCached; ++j) {
+    const int e = 64 * j + lane;
+    m[j] = e < n ? pm[e] : -INFINITY;
+    sm[j] = e < n ? ps[e] : 0.f;
+    tk[j] = e < n ? pt[e] : -1;
+  }
+  float mg = fmaxf(m[0], m[1]);
+  for (int e = 64 * kCached + lane; e < n; e += 64) mg = fmaxf(mg, pm[e]);
+  mg = wave_max(mg);
+  if (mg == -INFINITY) {  // no finite score in the row
+    if (lane == 0) a.tokens[row] = 0;
     return;
   }
-  auto weight = [&](int c) { return c < a.chunks && pm[c] != -INFINITY ? ps[c] * exp2f(pm[c] - Mg) : 0.f; };
-  float wsum = 0.f;
-  for (int c = tid; c < a.chunks; c += 256) wsum += weight(c);
-  const float W = block_sum256(wsum, red);
-  // two uniforms in (0, 1] for this row and call
-  const U4 r = philox10(U4{(uint32_t)a.offset, (uint32_t)(a.offset >> 32), (uint32_t)row, 1u},
-                        (uint32_t)a.seed, (uint32_t)(a.seed >> 32));
-  const float u1 = ((float)r.x + 1.0f) * 2.3283064365386963e-10f;
-  const float u2 = ((float)r.y + 1.0f) * 2.3283064365386963e-10f;
-  // chunk: the first whose running weight reaches u1 W (rounding: the last with weight)
-  const float t1 = u1 * W;
+  auto weight = [&](float mc, float sc) { return mc != -INFINITY ? sc * exp2f(mc - mg) : 0.f; };
+  float w[kCached], incl[kCached];
+  float total = 0.f;
+#pragma unroll
+  for (int j = 0; j < kCached; ++j) {
+    w[j] = weight(m[j], sm[j]);
+    incl[j] = wave_incl(w[j]);
+    total += __shfl(incl[j], 63);
+  }
+  for (int base = 64 * kCached; base < n; base += 64) {
+    const int e = base + lane;
+    total += __shfl(wave_incl(e < n ? weight(pm[e], ps[e]) : 0.f), 63);
+  }
+  float u, unused;
+  row_uniforms(a, (uint32_t)row, 1u, &u, &unused);
+  const float t = u * total;
+  // the first entry whose running weight reaches t (rounding: the last with weight)
+  int tok = -1, last = -1;
   float run = 0.f;
-  int pick = a.chunks, last_pos = -1;
-  for (int base = 0; base < a.chunks; base += 256) {
-    const int c = base + tid;
-    const float wc = weight(c);
-    float tot;
-    const float ex = block_excl256(wc, red, &tot);
-    const int hit = (wc > 0.f && run + ex + wc >= t1) ? c : a.chunks;
-    const int lp = wc > 0.f ? c : -1;
-    // smallest hit and largest positive chunk over the block
-    int h = hit, l = lp;
 #pragma unroll
-    for (int mm = 32; mm >= 1; mm >>= 1) {
-      h = min(h, __shfl_xor(h, mm));
-      l = max(l, __shfl_xor(l, mm));
-    }
-    __shared__ int s_h[4], s_l[4];
-    __syncthreads();
-    if ((tid & 63) == 0) { s_h[tid >> 6] = h; s_l[tid >> 6] = l; }
-    __syncthreads();
-    pick = min(pick, min(min(s_h[0], s_h[1]), min(s_h[2], s_h[3])));
-    last_pos = max(last_pos, max(max(s_l[0], s_l[1]), max(s_l[2], s_l[3])));
-    run += tot;
+  for (int j = 0; j < kCached; ++j) {
+    const uint64_t pos = __ballot(w[j] > 0.f);
+    const uint64_t hit = __ballot(w[j] > 0.f && run + incl[j] >= t);
+    if (pos) last = __shfl(tk[j], 63 - __builtin_clzll(pos));
+    if (tok < 0 && hit) tok = __shfl(tk[j], __builtin_ctzll(hit));
+    run += __shfl(incl[j], 63);
   }
-  if (pick >= a.chunks) pick = last_pos;
-  // element: the first of the chunk whose running mass reaches u2 S_c
-  const float Mc = pm[pick];
-  const float t2 = u2 * ps[pick];
-  const float scale = NVK_LOG2E / a.temperatures[row];
-  float e[32];  // the thread's 32 elements, in index order
-  float tsum = 0.f;
-  const int first = pick * kChunk + 32 * tid;
-  if (sizeof(T) == 2 && a.vec_ok && first + 32 <= a.vocab) {
-    // 64 bf16 bytes: the four 16-byte loads leave before the first wait
-    const uint16_t* p = static_cast<const uint16_t*>(a.logits) + (int64_t)row * a.row_stride + first;
-    nvk_u32x4 w[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = *reinterpret_cast<const nvk_u32x4*>(p + 8 * j);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t ww[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        e[8 * j + 2 * i] = exp2f(mass_x(nvk_bf16lo_to_f32(ww[i]), scale) - Mc);
-        e[8 * j + 2 * i + 1] = exp2f(mass_x(nvk_bf16hi_to_f32(ww[i]), scale) - Mc);
-        tsum += e[8 * j + 2 * i];
-        tsum += e[8 * j + 2 * i + 1];
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int base = first + 8 * j;
-      float l[8];
-      if (base < a.vocab) {
-        load8<T>(a, row, base, base + 8 <= a.vocab, l);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) l[i] = -INFINITY;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        e[8 * j + i] = exp2f(mass_x(l[i], scale) - Mc);
-        tsum += e[8 * j + i];
-      }
-    }
+  for (int base = 64 * kCached; tok < 0 && base < n; base += 64) {
+    const int e = base + lane;
+    const float we = e < n ? weight(pm[e], ps[e]) : 0.f;
+    const float ie = wave_incl(we);
+    const uint64_t pos = __ballot(we > 0.f);
+    const uint64_t hit = __ballot(we > 0.f && run + ie >= t);
+    const int te = e < n ? pt[e] : -1;
+    if (pos) last = __shfl(te, 63 - __builtin_clzll(pos));
+    if (hit) tok = __shfl(te, __builtin_ctzll(hit));
+    run += __shfl(ie, 63);
   }
-  float tot;
-  const float ex = block_excl256(tsum, red, &tot);
-  int found = a.vocab, lastpos = -1;
-  for (int i = 31; i >= 0; --i)
-    if (e[i] > 0.f) { lastpos = first + i; break; }
-  if (tsum > 0.f && ex < t2 && t2 <= ex + tsum) {  // the target falls in this thread's run
-    float cum = ex;
-    found = lastpos;  // if rounding keeps the running sum below the target
-    for (int i = 0; i < 32; ++i) {
-      cum += e[i];
-      if (e[i] > 0.f && cum >= t2) { found = first + i; break; }
-    }
-  }
-  int fnd = found, lst = lastpos;
-#pragma unroll
-  for (int mm = 32; mm >= 1; mm >>= 1) {
-    fnd = min(fnd, __shfl_xor(fnd, mm));
-    lst = max(lst, __shfl_xor(lst, mm));
-  }
-  __shared__ int s_f[4], s_ls[4];
-  __syncthreads();
-  if ((tid & 63) == 0) { s_f[tid >> 6] = fnd; s_ls[tid >> 6] = lst; }
-  __syncthreads();
-  if (tid == 0) {
-    int tok = min(min(s_f[0], s_f[1]), min(s_f[2], s_f[3]));
-    if (tok >= a.vocab) tok = max(max(s_ls[0], s_ls[1]), max(s_ls[2], s_ls[3]));
-    a.tokens[row] = tok < 0 ? 0 : tok;
-  }
+  if (tok < 0) tok = last;
+  if (lane == 0) a.tokens[row] = tok < 0 ? 0 : tok;
 }
 
 struct GatherArgs {
@@ -519,7 +463,7 @@ __global__ __launch_bounds__(256) void gather_last_kernel(GatherArgs a) {
 extern "C" size_t nvk_sample_workspace_size(int32_t batch, int32_t vocab) {
   if (batch <= 0 || vocab <= 0) return 0;
   const size_t chunks = ((size_t)vocab + kChunk - 1) / kChunk;
-  return (size_t)batch * chunks * 8;
+  return (size_t)batch * chunks * (kPartThreads / 64) * 12;
 }
 
 extern "C" int nvk_sample(const void* logits, int64_t row_stride, int32_t batch, int32_t vocab,
@@ -547,34 +491,27 @@ extern "C" int nvk_sample(const void* logits, int64_t row_stride, int32_t batch,
   a.noise_stride = noise_row_stride;
   a.seed = seed;
   a.offset = offset;
+  const size_t slots = (size_t)batch * a.chunks * (kPartThreads / 64);
   a.part_score = static_cast<float*>(workspace);
-  a.part_index = reinterpret_cast<int*>(static_cast<char*>(workspace) + need / 2);
+  a.part_index = reinterpret_cast<int*>(static_cast<char*>(workspace) + 4 * slots);
+  a.part_token = reinterpret_cast<int*>(static_cast<char*>(workspace) + 8 * slots);
   a.tokens = tokens;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(a.chunks, batch);
   const bool bf16 = dtype == NVK_DTYPE_BF16;
-  // The kernel's own randomness: the exponential race for small steps (one
-  // pass, its Philox draws per element cheap enough), inverse-CDF over the
-  // chunk masses for large ones (two draws per row; its pick kernel adds a
-  // fixed ~8 us).  Measured on MI355X, vocab 151936: B = 64 race 14.8 us,
-  // inverse-CDF 16.8 us; B = 512 race 58.5 us, inverse-CDF 45.4 us.
-  if (!noise && (int64_t)batch * vocab >= kCdfMinElements) {
-    if (bf16) hipLaunchKernelGGL((sample_mass_kernel<uint16_t>), grid, dim3(kPartThreads), 0, s, a);
-    else hipLaunchKernelGGL((sample_mass_kernel<float>), grid, dim3(kPartThreads), 0, s, a);
+  // The kernel's own randomness: inverse CDF (one read of the logits, one
+  // exp2 per element, two uniforms per 2048 elements and one per row).
+  if (!noise) {
+    if (bf16) hipLaunchKernelGGL((sample_draw_kernel<uint16_t>), grid, dim3(kPartThreads), 0, s, a);
+    else hipLaunchKernelGGL((sample_draw_kernel<float>), grid, dim3(kPartThreads), 0, s, a);
     int st = nvk_launch_status();
     if (st != NVK_OK) return st;
-    if (bf16) hipLaunchKernelGGL((sample_pick_kernel<uint16_t>), dim3(batch), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((sample_pick_kernel<float>), dim3(batch), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(sample_choose_kernel, dim3((batch + 3) / 4), dim3(256), 0, s, a, batch);
     return nvk_launch_status();
   }
-  if (bf16 && noise)
-    hipLaunchKernelGGL((sample_partial_kernel<uint16_t, true>), grid, dim3(kPartThreads), 0, s, a);
-  else if (bf16)
-    hipLaunchKernelGGL((sample_partial_kernel<uint16_t, false>), grid, dim3(kPartThreads), 0, s, a);
-  else if (noise)
-    hipLaunchKernelGGL((sample_partial_kernel<float, true>), grid, dim3(kPartThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL((sample_partial_kernel<float, false>), grid, dim3(kPartThreads), 0, s, a);
+  // The caller's noise: the race.
+  if (bf16) hipLaunchKernelGGL((sample_partial_kernel<uint16_t>), grid, dim3(kPartThreads), 0, s, a);
+  else hipLaunchKernelGGL((sample_partial_kernel<float>), grid, dim3(kPartThreads), 0, s, a);
   int st = nvk_launch_status();
   if (st != NVK_OK) return st;
   hipLaunchKernelGGL(sample_final_kernel, dim3((batch + 3) / 4), dim3(256), 0, s, a, batch);

@@ -2,11 +2,12 @@
 nanovllm/layers/embed_head.py:56-60 on MI355X.
 
 ``Sampler().forward(logits, temperatures)`` keeps the reference's signature
-and distribution: token = argmax softmax(logits / T) / Exp(1) noise, computed
-by libnvk.so (``nvk_sample``) in a single read of the logits (the softmax
-normaliser does not change the maximiser).  The noise comes from a
-Philox stream seeded from torch's CPU generator (so torch.manual_seed makes
-runs repeatable) or, for checking against a reference draw, from the caller.
+and distribution: token i with probability softmax(logits / T)_i, drawn by
+libnvk.so (``nvk_sample``) in a single read of the logits.  Without the
+caller's noise the draw is an inverse transform with uniforms from a Philox
+stream seeded from torch's CPU generator (so torch.manual_seed makes runs
+repeatable); with it (for checking against a reference draw) the reference's
+argmax softmax(logits / T) / noise itself is evaluated.
 
 ``last_token_hidden`` / ``compute_logits`` are ParallelLMHead.forward for one
 rank: in a prefill step only each sequence's last new token reaches the LM
@@ -41,7 +42,7 @@ class Sampler(nn.Module):
         tokens = torch.empty(b, dtype=torch.int64, device=dev)
         seed = int(torch.randint(0, 2 ** 62, (1,)).item()) if noise is None else 0
         offset = self._offset
-        self._offset += (v + 3) // 4 + 1
+        self._offset += 1
         lib = _lib.load()
         ws_bytes = lib.nvk_sample_workspace_size(b, v)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)

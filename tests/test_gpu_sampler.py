@@ -138,6 +138,57 @@ def test_draws_across_vocab_chunks_follow_softmax():
     assert stats.chisquare(counts, p * counts.sum()).pvalue > 1e-4
 
 
+def test_draws_inside_one_chunk_follow_softmax():
+    """Mass over every token of one 8192-token chunk, shuffled so that each
+    thread and pass of the chunk's workgroup holds some of it: the chunk's
+    own inverse-CDF draw follows the softmax (16 bins of 512 tokens)."""
+    say("sampler draws inside one chunk")
+    v, rows, calls, temp = 8192, 4096, 10, 1.3
+    perm = torch.randperm(v, generator=torch.Generator().manual_seed(3))
+    base = torch.linspace(-3.0, 3.0, v)[perm].to(torch.bfloat16)
+    logits = base.repeat(rows, 1).cuda()
+    temps = torch.full((rows,), temp, device="cuda")
+    toks = torch.cat([_raw_sample(logits, temps, 21, k * 3001) for k in range(calls)]).cpu().numpy()
+    x = base.float().numpy().astype(np.float64) / temp
+    p = np.exp(x - x.max())
+    p /= p.sum()
+    counts = np.bincount(toks // 512, minlength=16)
+    expected = np.bincount(np.arange(v) // 512, weights=p, minlength=16) * toks.size
+    assert stats.chisquare(counts, expected).pvalue > 1e-4
+
+
+def test_draws_over_a_full_vocabulary_follow_softmax():
+    """Qwen3-sized rows (151936 logits: 19 workgroups and 75 wave chunks of
+    2048 logits per row, the last ones partial), 10240 draws: the counts per
+    2048-token bin match the bins' softmax mass (chi-square: a dropped or
+    doubled bin fails it), the draws' summed log-probability matches minus
+    the rows' entropy (z-test: tokens mapped to the wrong index inside a bin
+    fail it), and the randomised probability integral transform of each draw,
+    F(token - 1) + v p(token) with v uniform, is uniform on (0, 1) (KS test)."""
+    say("sampler full-vocabulary draws")
+    v, rows, calls, temp = 151936, 512, 20, 1.0
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    logits = (torch.randn(rows, v, generator=gen, device="cuda") * 2).to(torch.bfloat16)
+    temps = torch.full((rows,), temp, device="cuda")
+    toks = torch.stack([_raw_sample(logits, temps, 41, k * 40000) for k in range(calls)], 1)
+    p = torch.softmax(logits.double() / temp, dim=-1)
+    nb = (v + 2047) // 2048
+    bin_of = torch.arange(v, device="cuda") // 2048
+    mass = torch.zeros(nb, dtype=torch.float64, device="cuda").index_add_(0, bin_of, p.sum(0))
+    counts = torch.bincount(bin_of[toks.flatten()], minlength=nb)
+    assert stats.chisquare(counts.cpu().numpy(), (mass * calls).cpu().numpy()).pvalue > 1e-4
+    lp = torch.log(p.clamp_min(1e-300))
+    ent = -(p * lp).sum(-1)
+    var = (p * lp * lp).sum(-1) - ent * ent
+    z = (lp.gather(1, toks).sum() + ent.sum() * calls) / torch.sqrt(var.sum() * calls)
+    assert abs(z.item()) < 5, z.item()
+    before = (torch.cumsum(p, dim=-1) - p).gather(1, toks)
+    vv = torch.rand(toks.shape, generator=torch.Generator(device="cuda").manual_seed(5),
+                    device="cuda", dtype=torch.float64)
+    pit = (before + vv * p.gather(1, toks)).flatten().cpu().numpy()
+    assert stats.kstest(pit, "uniform").pvalue > 1e-4
+
+
 def test_draws_uniform_over_a_partial_last_chunk():
     say("sampler partial last chunk")
     v = 8197                                                  # 8192 + 5

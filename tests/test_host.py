@@ -152,10 +152,10 @@ def test_error_codes_without_launching():
     assert lib.nvk_decode_metadata(16, 16, 16, 4, 8, 256, 4, 2, 16, 16, 16, 16, None) == -1
     assert lib.nvk_decode_metadata(None, None, None, 0, 0, 256, 0, 0, None, None, None, None,
                                    None) == 0
-    # sampler: one (score, index) pair per row and 8192-element chunk
-    assert lib.nvk_sample_workspace_size(64, 151936) == 64 * 19 * 8
+    # sampler: three 4-byte slots per row and 2048-element wave chunk
+    assert lib.nvk_sample_workspace_size(64, 151936) == 64 * 19 * 4 * 12
     assert lib.nvk_sample_workspace_size(0, 10) == 0
-    smp = [16, 151936, 64, 151936, 0, 16, None, 0, 1, 0, 16, 16, 64 * 19 * 8, None]
+    smp = [16, 151936, 64, 151936, 0, 16, None, 0, 1, 0, 16, 16, 64 * 19 * 48, None]
     assert lib.nvk_sample(*smp[:4], 1, *smp[5:]) == -2                     # fp16 logits
     small = list(smp); small[12] = 8
     assert lib.nvk_sample(*small) == -4                                    # workspace too small
