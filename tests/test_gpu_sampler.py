@@ -138,6 +138,27 @@ def test_draws_across_vocab_chunks_follow_softmax():
     assert stats.chisquare(counts, p * counts.sum()).pvalue > 1e-4
 
 
+def test_draws_over_more_than_128_wave_chunks():
+    """A 300000-token vocabulary (147 wave chunks of 2048 logits: the choose
+    kernel's registers hold 128, the rest go through its loop), mass on
+    tokens on both sides of the 128-chunk edge (262144) and at the last one."""
+    say("sampler draws past 128 wave chunks")
+    v, rows, calls = 300000, 1024, 10
+    hot = [5, 100000, 262143, 262144, 270000, 299999]
+    vals = torch.linspace(-0.8, 0.9, len(hot))
+    base = torch.full((v,), -40.0)
+    base[hot] = vals
+    logits = base.to(torch.bfloat16).repeat(rows, 1).cuda()
+    temps = torch.ones(rows, device="cuda")
+    toks = torch.cat([_raw_sample(logits, temps, 13, k * 7919) for k in range(calls)]).cpu().numpy()
+    assert np.isin(toks, hot).all()
+    counts = np.array([(toks == h).sum() for h in hot])
+    x = base.to(torch.bfloat16).float().numpy()[hot].astype(np.float64)
+    p = np.exp(x - x.max())
+    p /= p.sum()
+    assert stats.chisquare(counts, p * counts.sum()).pvalue > 1e-4
+
+
 def test_draws_inside_one_chunk_follow_softmax():
     """Mass over every token of one 8192-token chunk, shuffled so that each
     thread and pass of the chunk's workgroup holds some of it: the chunk's
