@@ -441,8 +441,9 @@ int nvk_uniform_cu_seqlens(const int32_t* seqlens_k, int32_t batch, int32_t seql
 /*
  * LM-head last-token gather (nanovllm/layers/embed_head.py:56-60): in a
  * prefill step, out[b] = x[cu_seqlens_q[b+1] - 1] (row b of [batch][hidden]
- * bf16, row strides in elements).  A sequence with cu_seqlens_q[b+1] == 0
- * leaves its output row unwritten.  hidden and strides multiples of 8.
+ * bf16 or f16 (dtype), row strides in elements).  A sequence with
+ * cu_seqlens_q[b+1] == 0 leaves its output row unwritten.  hidden and strides
+ * multiples of 8.
  */
 int nvk_gather_last_tokens(const void* x, int64_t x_row_stride, const int32_t* cu_seqlens_q,
                            int32_t batch, int32_t hidden, int32_t dtype, void* out,
@@ -461,7 +462,7 @@ int nvk_gather_last_tokens(const void* x, int64_t x_row_stride, const int32_t* c
  * w < 2 + ceil(vocab / 2048): calls that must draw independently use
  * different offsets.  Non-finite logits carry no mass.
  * Rows without a finite logit give token 0.
- * logits: bf16 or f32 [batch][row_stride]; tokens: int64 [batch].
+ * logits: bf16, f16 or f32 (dtype) [batch][row_stride]; tokens: int64 [batch].
  * workspace: nvk_sample_workspace_size() bytes (16-byte aligned; three 4-byte
  * slots per row and 2048 logits), need not be initialised.
  * Two kernels: one workgroup per row and 8192 logits, then one wave per row.

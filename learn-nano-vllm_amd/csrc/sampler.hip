@@ -60,7 +60,8 @@ __device__ __forceinline__ bool better(float s, int i, float bs, int bi) {
   return s > bs || (s == bs && i < bi);
 }
 
-template <typename T>
+// Logits of T = uint16_t (bf16, or f16 when F16) or float.
+template <typename T, bool F16>
 __device__ __forceinline__ void load8(const SampleArgs& a, int row, int base, bool full, float* l) {
   if constexpr (sizeof(T) == 2) {
     const uint16_t* p = static_cast<const uint16_t*>(a.logits) + (int64_t)row * a.row_stride + base;
@@ -69,13 +70,13 @@ __device__ __forceinline__ void load8(const SampleArgs& a, int row, int base, bo
       const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        l[2 * i] = nvk_bf16lo_to_f32(ww[i]);
-        l[2 * i + 1] = nvk_bf16hi_to_f32(ww[i]);
+        l[2 * i] = NvkElt<F16>::lo(ww[i]);
+        l[2 * i + 1] = NvkElt<F16>::hi(ww[i]);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        l[i] = (full || base + i < a.vocab) ? __uint_as_float((uint32_t)p[i] << 16) : -INFINITY;
+        l[i] = (full || base + i < a.vocab) ? NvkElt<F16>::lo((uint32_t)p[i]) : -INFINITY;
     }
   } else {
     const float* p = static_cast<const float*>(a.logits) + (int64_t)row * a.row_stride + base;
@@ -86,7 +87,7 @@ __device__ __forceinline__ void load8(const SampleArgs& a, int row, int base, bo
 
 // Race scores of one row chunk in log2 units: logits * log2(e) / T - log2(E),
 // E = max(noise, 1e-10) (the base change does not move the maximiser).
-template <typename T>
+template <typename T, bool F16>
 __global__ __launch_bounds__(kPartThreads) void sample_partial_kernel(SampleArgs a) {
   const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
   const float scale = NVK_LOG2E / a.temperatures[row];
@@ -113,7 +114,7 @@ __global__ __launch_bounds__(kPartThreads) void sample_partial_kernel(SampleArgs
       const uint32_t ww[4] = {w[it].x, w[it].y, w[it].z, w[it].w};
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float l = (i & 1) ? nvk_bf16hi_to_f32(ww[i >> 1]) : nvk_bf16lo_to_f32(ww[i >> 1]);
+        const float l = (i & 1) ? NvkElt<F16>::hi(ww[i >> 1]) : NvkElt<F16>::lo(ww[i >> 1]);
         const float sc = l * scale - __builtin_amdgcn_logf(fmaxf(nz[it][i], kMinNoise));
         // a thread visits its indices in increasing order: strictly greater wins
         if (sc > best) {
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(kPartThreads) void sample_partial_kernel(SampleArgs
       if (base >= a.vocab) break;
       const bool full = base + 8 <= a.vocab;
       float l[8];
-      load8<T>(a, row, base, full, l);
+      load8<T, F16>(a, row, base, full, l);
       const float* q = a.noise + (int64_t)row * a.noise_stride + base;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -284,7 +285,7 @@ __device__ __forceinline__ int first_reaching(const float (&cum)[32], float t) {
   return idx + (h2[0] < t ? 1 : 0);
 }
 
-template <typename T>
+template <typename T, bool F16>
 __global__ __launch_bounds__(kPartThreads) void sample_draw_kernel(SampleArgs a) {
   const int c = blockIdx.x, row = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -304,8 +305,8 @@ __global__ __launch_bounds__(kPartThreads) void sample_draw_kernel(SampleArgs a)
       const uint32_t ww[4] = {w[it].x, w[it].y, w[it].z, w[it].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        l[8 * it + 2 * i] = nvk_bf16lo_to_f32(ww[i]);
-        l[8 * it + 2 * i + 1] = nvk_bf16hi_to_f32(ww[i]);
+        l[8 * it + 2 * i] = NvkElt<F16>::lo(ww[i]);
+        l[8 * it + 2 * i + 1] = NvkElt<F16>::hi(ww[i]);
       }
     }
   } else {
@@ -313,7 +314,7 @@ __global__ __launch_bounds__(kPartThreads) void sample_draw_kernel(SampleArgs a)
     for (int it = 0; it < kIters; ++it) {
       const int base = first + it * kPartThreads * 8;
       if (base < a.vocab) {
-        load8<T>(a, row, base, base + 8 <= a.vocab, &l[8 * it]);
+        load8<T, F16>(a, row, base, base + 8 <= a.vocab, &l[8 * it]);
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) l[8 * it + i] = -INFINITY;
@@ -472,7 +473,8 @@ extern "C" int nvk_sample(const void* logits, int64_t row_stride, int32_t batch,
                           int64_t* tokens, void* workspace, size_t workspace_bytes,
                           void* stream) {
   if (batch < 0 || vocab <= 0 || row_stride < vocab) return NVK_EINVAL;
-  if (dtype != NVK_DTYPE_BF16 && dtype != NVK_DTYPE_F32) return NVK_EUNSUPPORTED;
+  if (dtype != NVK_DTYPE_BF16 && dtype != NVK_DTYPE_F16 && dtype != NVK_DTYPE_F32)
+    return NVK_EUNSUPPORTED;
   if (batch == 0) return NVK_OK;
   if (batch > 65535) return NVK_EUNSUPPORTED;
   if (!logits || !temperatures || !tokens) return NVK_EINVAL;
@@ -498,20 +500,27 @@ extern "C" int nvk_sample(const void* logits, int64_t row_stride, int32_t batch,
   a.tokens = tokens;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(a.chunks, batch);
-  const bool bf16 = dtype == NVK_DTYPE_BF16;
   // The kernel's own randomness: inverse CDF (one read of the logits, one
   // exp2 per element, two uniforms per 2048 elements and one per row).
   if (!noise) {
-    if (bf16) hipLaunchKernelGGL((sample_draw_kernel<uint16_t>), grid, dim3(kPartThreads), 0, s, a);
-    else hipLaunchKernelGGL((sample_draw_kernel<float>), grid, dim3(kPartThreads), 0, s, a);
+    if (dtype == NVK_DTYPE_BF16)
+      hipLaunchKernelGGL((sample_draw_kernel<uint16_t, false>), grid, dim3(kPartThreads), 0, s, a);
+    else if (dtype == NVK_DTYPE_F16)
+      hipLaunchKernelGGL((sample_draw_kernel<uint16_t, true>), grid, dim3(kPartThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((sample_draw_kernel<float, false>), grid, dim3(kPartThreads), 0, s, a);
     int st = nvk_launch_status();
     if (st != NVK_OK) return st;
     hipLaunchKernelGGL(sample_choose_kernel, dim3((batch + 3) / 4), dim3(256), 0, s, a, batch);
     return nvk_launch_status();
   }
   // The caller's noise: the race.
-  if (bf16) hipLaunchKernelGGL((sample_partial_kernel<uint16_t>), grid, dim3(kPartThreads), 0, s, a);
-  else hipLaunchKernelGGL((sample_partial_kernel<float>), grid, dim3(kPartThreads), 0, s, a);
+  if (dtype == NVK_DTYPE_BF16)
+    hipLaunchKernelGGL((sample_partial_kernel<uint16_t, false>), grid, dim3(kPartThreads), 0, s, a);
+  else if (dtype == NVK_DTYPE_F16)
+    hipLaunchKernelGGL((sample_partial_kernel<uint16_t, true>), grid, dim3(kPartThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((sample_partial_kernel<float, false>), grid, dim3(kPartThreads), 0, s, a);
   int st = nvk_launch_status();
   if (st != NVK_OK) return st;
   hipLaunchKernelGGL(sample_final_kernel, dim3((batch + 3) / 4), dim3(256), 0, s, a, batch);
@@ -524,7 +533,7 @@ extern "C" int nvk_gather_last_tokens(const void* x, int64_t x_row_stride,
                                       void* stream) {
   if (batch < 0 || hidden <= 0 || x_row_stride < hidden || out_row_stride < hidden)
     return NVK_EINVAL;
-  if (dtype != NVK_DTYPE_BF16) return NVK_EUNSUPPORTED;
+  if (dtype != NVK_DTYPE_BF16 && dtype != NVK_DTYPE_F16) return NVK_EUNSUPPORTED;  // 16-bit rows
   if (batch == 0) return NVK_OK;
   if (!x || !cu_seqlens_q || !out) return NVK_EINVAL;
   if (((uintptr_t)x | (uintptr_t)out) % 16 || (hidden % 8) || (x_row_stride % 8) ||

@@ -33,7 +33,8 @@ def _check_tokens(got, logits_np, temps, noise):
 
 
 @pytest.mark.parametrize("b,v,dtype", [(64, 151936, torch.bfloat16), (5, 1000, torch.float32),
-                                       (3, 7, torch.bfloat16), (512, 4099, torch.bfloat16)])
+                                       (3, 7, torch.bfloat16), (512, 4099, torch.bfloat16),
+                                       (64, 151936, torch.float16), (7, 300, torch.float16)])
 def test_sampler_with_given_noise_matches_reference_formula(b, v, dtype):
     say(f"sampler given noise b={b} v={v} {dtype}")
     g = torch.Generator().manual_seed(b * 31 + v)
@@ -159,14 +160,16 @@ def test_draws_over_more_than_128_wave_chunks():
     assert stats.chisquare(counts, p * counts.sum()).pvalue > 1e-4
 
 
-def test_draws_inside_one_chunk_follow_softmax():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_draws_inside_one_chunk_follow_softmax(dtype):
     """Mass over every token of one 8192-token chunk, shuffled so that each
     thread and pass of the chunk's workgroup holds some of it: the chunk's
-    own inverse-CDF draw follows the softmax (16 bins of 512 tokens)."""
-    say("sampler draws inside one chunk")
+    own inverse-CDF draw follows the softmax (16 bins of 512 tokens), for
+    bf16 and fp16 logits."""
+    say(f"sampler draws inside one chunk {dtype}")
     v, rows, calls, temp = 8192, 4096, 10, 1.3
     perm = torch.randperm(v, generator=torch.Generator().manual_seed(3))
-    base = torch.linspace(-3.0, 3.0, v)[perm].to(torch.bfloat16)
+    base = torch.linspace(-3.0, 3.0, v)[perm].to(dtype)
     logits = base.repeat(rows, 1).cuda()
     temps = torch.full((rows,), temp, device="cuda")
     toks = torch.cat([_raw_sample(logits, temps, 21, k * 3001) for k in range(calls)]).cpu().numpy()
@@ -224,18 +227,26 @@ def test_draws_uniform_over_a_partial_last_chunk():
     assert abs((toks >= 8192).mean() - 5 / v) < 5 * np.sqrt(5 / v / toks.size)
 
 
-def test_rows_without_finite_logits_give_token_zero():
-    logits = torch.full((3, 100), float("-inf"), device="cuda")
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_rows_without_finite_logits_give_token_zero(dtype):
+    """Rows of -inf give token 0; NaN and +inf logits carry no mass (row 3:
+    its one finite logit is drawn)."""
+    logits = torch.full((4, 100), float("-inf"), device="cuda", dtype=dtype)
     logits[1, 37] = 0.0
-    out = _raw_sample(logits, torch.ones(3, device="cuda"), 1, 0).cpu().tolist()
-    assert out == [0, 37, 0]
+    logits[3, 5] = float("nan")
+    logits[3, 50] = float("inf")
+    logits[3, 60] = 0.5
+    for seed in (1, 2, 3):
+        out = _raw_sample(logits, torch.ones(4, device="cuda"), seed, 0).cpu().tolist()
+        assert out == [0, 37, 0, 60]
 
 
-def test_last_token_gather_and_lm_head():
-    say("lm head gather")
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_last_token_gather_and_lm_head(dtype):
+    say(f"lm head gather {dtype}")
     g = torch.Generator().manual_seed(3)
-    x = torch.randn(7, 1024, generator=g).to(torch.bfloat16).cuda()
-    w = torch.randn(300, 1024, generator=g).to(torch.bfloat16).cuda()
+    x = torch.randn(7, 1024, generator=g).to(dtype).cuda()
+    w = torch.randn(300, 1024, generator=g).to(dtype).cuda()
     cu = torch.tensor([0, 2, 3, 7], dtype=torch.int32, device="cuda")
     rows = last_token_hidden(x, cu)
     assert torch.equal(rows.cpu(), x.cpu()[[1, 2, 6]])

@@ -156,7 +156,7 @@ def test_error_codes_without_launching():
     assert lib.nvk_sample_workspace_size(64, 151936) == 64 * 19 * 4 * 12
     assert lib.nvk_sample_workspace_size(0, 10) == 0
     smp = [16, 151936, 64, 151936, 0, 16, None, 0, 1, 0, 16, 16, 64 * 19 * 48, None]
-    assert lib.nvk_sample(*smp[:4], 1, *smp[5:]) == -2                     # fp16 logits
+    assert lib.nvk_sample(*smp[:4], 7, *smp[5:]) == -2                     # unknown dtype
     small = list(smp); small[12] = 8
     assert lib.nvk_sample(*small) == -4                                    # workspace too small
     narrow = list(smp); narrow[1] = 100
