@@ -45,9 +45,10 @@ struct SampleArgs {
   const float* noise;  // null: the kernel's own draw (Philox)
   int64_t noise_stride;
   uint64_t seed, offset;
-  float* part_score;  // [batch][chunks]: the race's best score, or M_c
-  int* part_index;    // [batch][chunks]: the race's best index, or S_c (float bits)
-  int* part_token;    // [batch][chunks]: the chunk's drawn token (inverse CDF)
+  // per workgroup chunk [batch][chunks] (race) or wave chunk [batch][4 chunks] (draw):
+  float* part_score;  // the best score, or M_w
+  int* part_index;    // the best index, or S_w (float bits)
+  int* part_token;    // the wave chunk's drawn token (draw only)
   int64_t* tokens;
 };
 
