@@ -73,6 +73,7 @@ struct PrefillArgs {
   float scale_log2;
   uint16_t* out;
   int64_t out_stride_tok, out_stride_head;
+  int out_rows16;  // out 16-byte aligned, strides multiples of 8: whole-row stores
   int n_qtiles;
   // Split-K over key tiles (short query ranges over long contexts): blockIdx.z
   // = qtile * n_splits + split, split j owning key tiles
@@ -904,10 +905,10 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     }
   }
 
-  // ---- epilogue: normalise and store the row -----------------------------------
-  if (!row_valid) return;
-  const float l_tot = nvk_sum_xor32(l_part[0] + l_part[1]);
+  // ---- epilogue: normalise and store the rows ----------------------------------
   if (a.n_splits > 1) {  // partial record: O^T column (unnormalised), m_ref, l
+    if (!row_valid) return;
+    const float l_tot = nvk_sum_xor32(l_part[0] + l_part[1]);
     float* rec = a.ws + ((((int64_t)s * a.num_kv_heads + kvh) * a.n_qtiles + qt) * a.n_splits +
                          split) * (int64_t)kRows * kRecFloats +
                  (int64_t)row * kRecFloats;
@@ -926,18 +927,55 @@ __global__ __launch_bounds__(64 * kWaves, 8 / kWaves) void varlen_prefill_kernel
     }
     return;
   }
+  const float l_tot = nvk_sum_xor32(l_part[0] + l_part[1]);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  uint16_t* op = a.out + ((int64_t)q_row0 + tok) * a.out_stride_tok + (int64_t)head * a.out_stride_head;
+  // Lane (half, l32) holds d = 32 db + 8 grp + 4 half .. +3 of its row.
+  auto packed = [&](int db, int grp) {
+    nvk_u32x2 w;
+    w.x = E::pack2(acc_o[db][4 * grp] * inv, acc_o[db][4 * grp + 1] * inv);
+    w.y = E::pack2(acc_o[db][4 * grp + 2] * inv, acc_o[db][4 * grp + 3] * inv);
+    return w;
+  };
+  if (!a.out_rows16) {  // 8 bytes per lane and store (16 per row and instruction)
+    if (!row_valid) return;
+    uint16_t* op = a.out + ((int64_t)q_row0 + tok) * a.out_stride_tok + (int64_t)head * a.out_stride_head;
 #pragma unroll
-  for (int db = 0; db < HD / 32; ++db) {
+    for (int db = 0; db < HD / 32; ++db)
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp)
+        *reinterpret_cast<nvk_u32x2*>(op + 32 * db + 8 * grp + 4 * half) = packed(db, grp);
+    return;
+  }
+  // The wave's 32 rows go through its own HD * 64 bytes of the K stages, so
+  // that each store writes four whole rows (half as many store instructions,
+  // every 128-byte line written whole).  No wave reads a K stage in a range's
+  // last step, and the stages' last loads were awaited before that step's
+  // barrier.  16-byte chunk c of row r sits at chunk c ^ (r & 15): two-way
+  // bank conflicts on the writes, none on the reads.
+  constexpr uint32_t kRowB = HD * 2;
+  const uint32_t ebase = lds_base + (uint32_t)wave * 32u * kRowB;
+  typedef __attribute__((address_space(3))) nvk_u32x2 lds_u32x2;
+  typedef __attribute__((address_space(3))) nvk_u32x4 lds_u32x4;
+#pragma unroll
+  for (int db = 0; db < HD / 32; ++db)
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
-      const int d = 32 * db + 8 * grp + 4 * half;
-      nvk_u32x2 w;
-      w.x = E::pack2(acc_o[db][4 * grp] * inv, acc_o[db][4 * grp + 1] * inv);
-      w.y = E::pack2(acc_o[db][4 * grp + 2] * inv, acc_o[db][4 * grp + 3] * inv);
-      *reinterpret_cast<nvk_u32x2*>(op + d) = w;
+      const uint32_t c = (uint32_t)((4 * db + grp) ^ (l32 & 15));
+      *(lds_u32x2*)(size_t)(ebase + (uint32_t)l32 * kRowB + 16u * c + 8u * (uint32_t)half) =
+          packed(db, grp);
     }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const int c = lane & 15;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int rr = 4 * j + (lane >> 4);
+    const nvk_u32x4 v = *(lds_u32x4*)(size_t)(ebase + (uint32_t)rr * kRowB +
+                                               16u * (uint32_t)(c ^ (rr & 15)));
+    const int r_row = wave * 32 + rr;
+    const int r_tok = q0 + r_row / G;
+    if (r_tok >= 0 && r_tok < Lq)
+      *reinterpret_cast<nvk_u32x4*>(a.out + ((int64_t)q_row0 + r_tok) * a.out_stride_tok +
+                                    (int64_t)(kvh * G + r_row % G) * a.out_stride_head + 8 * c) = v;
   }
 }
 
@@ -1239,6 +1277,7 @@ int varlen_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_he
   a.out = static_cast<uint16_t*>(out);
   a.out_stride_tok = out_stride_tok;
   a.out_stride_head = out_stride_head;
+  a.out_rows16 = (uintptr_t)out % 16 == 0 && out_stride_tok % 8 == 0 && out_stride_head % 8 == 0;
   a.n_qtiles = sp.n_qtiles;
   a.n_splits = sp.n_splits;
   a.tiles_per_split = sp.n_splits > 1 ? sp.tiles_per_split : 1 << 30;
