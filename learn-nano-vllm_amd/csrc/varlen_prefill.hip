@@ -33,6 +33,12 @@
 //     v_dot2_f32_bf16 over the packed probabilities.
 //   * The grid runs the query tiles nearest the end of each sequence (the
 //     ones with most keys) first.
+//   * The normalised output rows go back through LDS (each wave's 32 rows in
+//     the K stages, free in a range's last step), so each store writes four
+//     whole 256-byte rows.  Stored straight from the accumulator layout, a
+//     lane wrote 8 bytes to 16 places and each store covered 16 bytes of 32
+//     rows; the workgroup's end, and with it the start of the next one in its
+//     slot, waited for those partial-line writes.
 #include <type_traits>
 
 #include "nvk_common.h"
