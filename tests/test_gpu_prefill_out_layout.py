@@ -24,32 +24,34 @@ def _prefill_into(out, q, kc, vc, bt, cu_q, cu_k, max_q, max_k, hkv=8):
                                 vc.data_ptr(), 0, 0, 0, nb * bs, cu_q.data_ptr(), cu_k.data_ptr(),
                                 batch, max_q, max_k, bt.data_ptr(), bt.stride(0), bt.shape[1], bs,
                                 nb, hq, hkv, d, 128 ** -0.5, out.data_ptr(), out.stride(0),
-                                out.stride(1), None, 0, 0, torch.cuda.current_stream().cuda_stream)
+                                out.stride(1), None, 0, _lib.dtype_code(q),
+                                torch.cuda.current_stream().cuda_stream)
     assert rc == 0, lib.nvk_strerror(rc)
     torch.cuda.synchronize()
 
 
-def test_whole_row_and_per_lane_stores_agree():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_whole_row_and_per_lane_stores_agree(dtype):
     rng = np.random.default_rng(95)
     lens_q = [int(x) for x in rng.integers(1, 300, 10)] + [0, 1, 64, 65]
     lens_k = [q + int(c) for q, c in zip(lens_q, rng.integers(0, 400, len(lens_q)))]
     q, kc, vc, bt, cu_q, cu_k = _paged_case(96, lens_q, lens_k)
     tq, hq, d = q.shape
-    args = (q.cuda(), kc.cuda(), vc.cuda(), bt.cuda(), cu_q.cuda(), cu_k.cuda(), max(lens_q),
-            max(lens_k))
+    dq, dkc, dvc = (x.to(dtype).cuda() for x in (q, kc, vc))
+    args = (dq, dkc, dvc, bt.cuda(), cu_q.cuda(), cu_k.cuda(), max(lens_q), max(lens_k))
     nan = float("nan")
     # 16-byte aligned, contiguous: whole-row stores
-    aligned = torch.full((tq, hq, d), nan, dtype=torch.bfloat16, device="cuda")
+    aligned = torch.full((tq, hq, d), nan, dtype=dtype, device="cuda")
     say("prefill output: aligned rows")
     _prefill_into(aligned, *args)
     # 8-byte aligned (4 elements into a buffer): per-lane stores
-    buf = torch.full((tq * hq * d + 8,), nan, dtype=torch.bfloat16, device="cuda")
+    buf = torch.full((tq * hq * d + 8,), nan, dtype=dtype, device="cuda")
     shifted = buf[4:4 + tq * hq * d].view(tq, hq, d)
     assert shifted.data_ptr() % 16 == 8
     say("prefill output: shifted by 8 bytes")
     _prefill_into(shifted, *args)
     # head stride 132 (a multiple of 4, not of 8): per-lane stores
-    wide = torch.full((tq, hq, 132), nan, dtype=torch.bfloat16, device="cuda")
+    wide = torch.full((tq, hq, 132), nan, dtype=dtype, device="cuda")
     padded = wide[:, :, :d]
     say("prefill output: head stride 132")
     _prefill_into(padded, *args)
@@ -60,5 +62,6 @@ def test_whole_row_and_per_lane_stores_agree():
     # nothing written outside the output rows
     assert torch.isnan(buf[:4].float()).all() and torch.isnan(buf[4 + tq * hq * d:].float()).all()
     assert torch.isnan(wide[:, :, d:].float()).all()
-    ref = oracle_prefill_paged(q, kc, vc, bt, cu_q, cu_k, 256, 128 ** -0.5)
-    assert_attn_close(aligned, ref, "prefill, aligned output rows")
+    if dtype == torch.bfloat16:  # (fp16 prefill parity: test_gpu_fp16.py)
+        ref = oracle_prefill_paged(q, kc, vc, bt, cu_q, cu_k, 256, 128 ** -0.5)
+        assert_attn_close(aligned, ref, "prefill, aligned output rows")
